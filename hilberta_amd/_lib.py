@@ -35,30 +35,18 @@ SIGNATURES = {
          _c_int, _c_int, _c_f32, _p, _c_i64, _c_int, _p],
     ),
     "hb_gather_rows": (
-        _c_int,
-        [_p, _p, _p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _p],
+        _c_int, [_p, _p, _p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _p, _p],
     ),
-    "hb_pair_tables": (
+    "hb_hilbert_order": (_c_int, [_c_int, _p, _p]),
+    "hb_plan_layout": (_c_int, [_c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p, _p, _p, _p, _p]),
+    "hb_plan_scratch_bytes": (_c_i64, [_c_int, _c_int]),
+    "hb_plan_phase_bits": (
         _c_int,
-        [_p, _p, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _p],
+        [_p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p],
     ),
-    "hb_plan_layout": (
-        _c_int,
-        [_c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p, _p, _p, _p],
-    ),
-    "hb_plan_phase_adjacency": (
-        _c_int,
-        [_p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p, _p,
-         _p],
-    ),
-    "hb_adjacency_tables": (
-        _c_int,
-        [_p, _c_int, _c_int, _c_int, _p, _p, _p, _p, _p, _p, _p],
-    ),
-    "hb_emit_tables": (
-        _c_int,
-        [_p, _p, _p, _c_int, _c_int, _c_int, _p, _p, _p],
-    ),
+    "hb_table_bits": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _p, _p]),
+    "hb_bits_counts": (_c_int, [_p, _c_int, _c_int, _c_int, _p, _p, _p, _p]),
+    "hb_bits_emit": (_c_int, [_p, _c_int, _c_int, _c_int, _p, _c_int, _p, _p, _c_int, _p]),
 }
 
 _lib = None

@@ -1,0 +1,154 @@
+"""Drives the HIP block-table builder (csrc/tables.hip) through the C ABI.
+
+All integer work runs on the GPU.  The only host synchronisations are the ones the table format
+forces at setup time: the number of shared blocks of the layout (it sizes the global prefix) and
+the widest row of each emitted table (it is the table width).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+
+def _dev(device):
+    if device is None:
+        return torch.device("cuda", torch.cuda.current_device())
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise ValueError("the table builder runs on a HIP device (cuda:N); there is no CPU path")
+    return device
+
+
+@dataclass
+class DeviceLayout:
+    """Composite Hilbert order and physical packing, resident on the device."""
+
+    grid_size: int
+    block_size: int
+    text_tokens: int
+    shared_blocks: int
+    original_order: torch.Tensor
+    inverse_original: torch.Tensor
+    image_order: torch.Tensor
+    inverse_image_order: torch.Tensor
+    physical_original_blocks: torch.Tensor
+    original_to_physical: torch.Tensor
+
+    @property
+    def image_tokens(self):
+        return self.grid_size**2
+
+    @property
+    def image_blocks(self):
+        return self.image_tokens // self.block_size
+
+    @property
+    def text_blocks(self):
+        return self.text_tokens // self.block_size
+
+    @property
+    def global_blocks(self):
+        return self.text_blocks + self.shared_blocks
+
+    @property
+    def total_blocks(self):
+        return self.text_blocks + self.image_blocks
+
+    @property
+    def ordinary_blocks(self):
+        return self.total_blocks - self.global_blocks
+
+    @property
+    def words(self):
+        return (self.total_blocks + 31) // 32
+
+
+def hilbert_order_device(grid_size, device=None):
+    device = _dev(device)
+    out = torch.empty(grid_size * grid_size, dtype=torch.int64, device=device)
+    _lib.check(_lib.load().hb_hilbert_order(grid_size, out.data_ptr(), _lib.stream_ptr(device)),
+               "hb_hilbert_order")
+    return out
+
+
+def layout_device(grid_size, block_size, text_tokens, shared, device=None):
+    device = _dev(device)
+    lib = _lib.load()
+    n = grid_size * grid_size
+    nb = n // block_size
+    i64 = dict(dtype=torch.int64, device=device)
+    t = [torch.empty(n, **i64) for _ in range(4)] + [torch.empty(nb, **i64) for _ in range(2)]
+    status = torch.zeros(2, dtype=torch.int32, device=device)
+    rc = lib.hb_plan_layout(grid_size, block_size, text_tokens, int(bool(shared)),
+                            *[x.data_ptr() for x in t], status.data_ptr(), _lib.stream_ptr(device))
+    _lib.check(rc, "hb_plan_layout")
+    n_shared, partial = status.tolist()  # setup-time sync: the prefix length is data dependent
+    if partial:
+        raise ValueError("Shared square must be a union of complete original blocks")
+    return DeviceLayout(grid_size, block_size, text_tokens, n_shared, *t)
+
+
+def phase_bits_device(layout: DeviceLayout, tile_count, phase, bridge_mode, k, scratch=None):
+    """Adjacency bitmap [ordinary, words] (int32 storage of uint32 words) and chosen bridges [nb, k]."""
+    device = layout.original_order.device
+    lib = _lib.load()
+    kk = max(int(k), 1)
+    bits = torch.empty((layout.ordinary_blocks, layout.words), dtype=torch.int32, device=device)
+    chosen = torch.full((layout.image_blocks, kk), -1, dtype=torch.int64, device=device)
+    if bridge_mode and scratch is None:
+        scratch = torch.empty(layout.image_blocks**2, dtype=torch.int32, device=device)
+    rc = lib.hb_plan_phase_bits(
+        layout.inverse_original.data_ptr(), layout.physical_original_blocks.data_ptr(),
+        layout.original_to_physical.data_ptr(), layout.grid_size, tile_count, layout.text_tokens,
+        layout.block_size, layout.shared_blocks, phase, bridge_mode, kk,
+        scratch.data_ptr() if bridge_mode else None, chosen.data_ptr(), bits.data_ptr(),
+        _lib.stream_ptr(device),
+    )
+    _lib.check(rc, "hb_plan_phase_bits")
+    return bits, chosen
+
+
+def emit_device(bits, total_blocks, *, unpaired=True, paired=False, key_block_size=64):
+    """Tables from a bitmap: returns dict with ids/counts and/or paired ids/flags/counts (device)."""
+    device = bits.device
+    lib = _lib.load()
+    rows = bits.shape[0]
+    i32 = dict(dtype=torch.int32, device=device)
+    counts = torch.empty(rows, **i32) if unpaired else None
+    pcounts = torch.empty(rows // 2, **i32) if paired else None
+    maxc = torch.zeros(2, **i32)
+    stream = _lib.stream_ptr(device)
+    rc = lib.hb_bits_counts(bits.data_ptr(), rows, total_blocks, key_block_size,
+                            counts.data_ptr() if unpaired else None,
+                            pcounts.data_ptr() if paired else None, maxc.data_ptr(), stream)
+    _lib.check(rc, "hb_bits_counts")
+    width, pwidth = (max(x, 1) for x in maxc.tolist())  # setup-time sync: table widths
+    ids = torch.empty((rows, width), **i32) if unpaired else None
+    pids = torch.empty((rows // 2, pwidth), **i32) if paired else None
+    pflags = torch.empty((rows // 2, pwidth), **i32) if paired else None
+    rc = lib.hb_bits_emit(bits.data_ptr(), rows, total_blocks, key_block_size,
+                          ids.data_ptr() if unpaired else None, width,
+                          pids.data_ptr() if paired else None, pflags.data_ptr() if paired else None,
+                          pwidth, stream)
+    _lib.check(rc, "hb_bits_emit")
+    out = {}
+    if unpaired:
+        out.update(kv_indices=ids, kv_counts=counts)
+    if paired:
+        out.update(paired_indices=pids, paired_flags=pflags, paired_counts=pcounts)
+    return out
+
+
+def table_bits_device(kv_indices, kv_counts, total_blocks):
+    device = kv_indices.device
+    rows, width = kv_indices.shape
+    words = (total_blocks + 31) // 32
+    bits = torch.empty((rows, words), dtype=torch.int32, device=device)
+    rc = _lib.load().hb_table_bits(kv_indices.data_ptr(), kv_counts.data_ptr(), rows, width,
+                                   total_blocks, bits.data_ptr(), _lib.stream_ptr(device))
+    _lib.check(rc, "hb_table_bits")
+    return bits

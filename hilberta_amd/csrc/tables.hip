@@ -1,0 +1,483 @@
+// Device construction of HilbertA block tables (integer-only, deterministic, bit-exact).
+//
+// Replaces the CPU setup of the reference (hilberta/geometry.py, plan.py:114-212,
+// bridge_k.py:10-51, paired_metadata.py:26-51) with gfx950 kernels.  The intermediate form is a
+// per-phase adjacency bitmap over physical 64-token blocks, one row of ceil(T/32) words for each
+// ordinary query block:
+//
+//   layout   composite Hilbert order cat(h[n/4:3n/4], n-1-h[n/4:3n/4]), its inverse, the optional
+//            shared centre square moved to the global prefix (plan.py:133-150, :186-197)
+//   bits     row of ordinary block o = global prefix | ordinary blocks with o's tile label
+//            (plan.py:173-183) | bridges: top-K key blocks of each query block ranked by
+//            (-score, (key - offset/bs) mod nb), where score counts cross-tile 4-neighbour token
+//            pairs between the two blocks in both directions (plan.py:159-172, bridge_k.py:22-43);
+//            directed (build_plan) or reciprocal (bridge_k: adj | adj^T, bridge_k.py:44)
+//   emit     rows of set bits in ascending order, zero padded to the widest row; paired rows merge
+//            query blocks 2r and 2r+1 with flag bit (half + 2*key_half) (paired_metadata.py:38-51)
+//
+// Integer atomics only (order-independent sums and ORs), so results do not depend on scheduling.
+#include "common.h"
+#include "../../include/hilberta_hip.h"
+
+namespace hb {
+namespace {
+
+constexpr int TPB = 256;
+
+__device__ __forceinline__ int64_t hilbert_raster(int64_t d, int g) {
+  // geometry.py:6-25: d2xy with the quadrant rotation, then raster id (g-1-y)*g + x
+  int64_t x = 0, y = 0, t = d;
+  for (int s = 1; s < g; s *= 2) {
+    const int64_t rx = (t / 2) & 1;
+    const int64_t ry = (t ^ (t / 2)) & 1;
+    if (ry == 0) {
+      if (rx) {
+        x = s - 1 - x;
+        y = s - 1 - y;
+      }
+      const int64_t tmp = x;
+      x = y;
+      y = tmp;
+    }
+    x += s * rx;
+    y += s * ry;
+    t /= 4;
+  }
+  return (int64_t)(g - 1 - y) * g + x;
+}
+
+__global__ void hilbert_kernel(int g, int64_t* out) {
+  const int64_t n = (int64_t)g * g;
+  for (int64_t d = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; d < n; d += (int64_t)gridDim.x * blockDim.x)
+    out[d] = hilbert_raster(d, g);
+}
+
+// original[i] = h[n/4 + i] (i < n/2), n-1-h[n/4 + i - n/2] (i >= n/2); inverse[original[i]] = i.
+__global__ void composite_kernel(int g, int64_t* original, int64_t* inverse) {
+  const int64_t n = (int64_t)g * g;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t half = n / 2;
+    const int64_t src = n / 4 + (i < half ? i : i - half);
+    const int64_t h = hilbert_raster(src, g);
+    const int64_t tok = i < half ? h : n - 1 - h;
+    original[i] = tok;
+    inverse[tok] = i;
+  }
+}
+
+// One workgroup: classify original blocks as shared (inside the centre square) or ordinary, then
+// pack them stably: shared blocks first (plan.py:138-150).  status[0] = #shared, [1] = partial.
+__global__ void __launch_bounds__(1024) pack_blocks_kernel(int g, int bs, int shared,
+                                                           const int64_t* original, int text_blocks,
+                                                           int64_t* packed, int64_t* to_physical,
+                                                           int32_t* status) {
+  const int64_t n = (int64_t)g * g;
+  const int nb = (int)(n / bs);
+  __shared__ int s_total[2];
+  __shared__ int s_scan[1024];
+  const int t = threadIdx.x;
+  const int per = (nb + 1023) / 1024;  // contiguous run of blocks per thread keeps the order stable
+  const int lo = min(t * per, nb), hi = min(lo + per, nb);
+  const int start = 3 * g / 8, end = 5 * g / 8;
+  int my_shared = 0, partial = 0;
+  for (int b = lo; b < hi; ++b) {
+    int cnt = 0;
+    if (shared) {
+      for (int j = 0; j < bs; ++j) {
+        const int64_t tok = original[(int64_t)b * bs + j];
+        const int y = (int)(tok / g), x = (int)(tok % g);
+        cnt += (y >= start && y < end && x >= start && x < end);
+      }
+    }
+    if (cnt != 0 && cnt != bs) partial = 1;
+    my_shared += (cnt == bs);
+  }
+  s_scan[t] = my_shared;
+  if (t == 0) s_total[1] = 0;
+  __syncthreads();
+  if (partial) atomicOr(&s_total[1], 1);
+  // inclusive scan of shared counts (Hillis-Steele)
+  for (int off = 1; off < 1024; off *= 2) {
+    const int v = t >= off ? s_scan[t - off] : 0;
+    __syncthreads();
+    s_scan[t] += v;
+    __syncthreads();
+  }
+  const int n_shared = s_scan[1023];
+  int sh_before = s_scan[t] - my_shared;
+  int ord_before = lo - sh_before;  // ordinary blocks before this thread's run
+  for (int b = lo; b < hi; ++b) {
+    int cnt = 0;
+    if (shared) {
+      for (int j = 0; j < bs; ++j) {
+        const int64_t tok = original[(int64_t)b * bs + j];
+        const int y = (int)(tok / g), x = (int)(tok % g);
+        cnt += (y >= start && y < end && x >= start && x < end);
+      }
+    }
+    int slot;
+    if (cnt == bs) slot = sh_before++;
+    else slot = n_shared + ord_before++;
+    packed[slot] = b;
+    to_physical[b] = slot + text_blocks;
+  }
+  if (t == 0) {
+    status[0] = n_shared;
+    status[1] = s_total[1];
+  }
+}
+
+// image_order[j*bs + u] = original[packed[j]*bs + u]; inverse_image_order[image_order[i]] = i
+__global__ void image_order_kernel(int64_t n, int bs, const int64_t* original, const int64_t* packed,
+                                   int64_t* order, int64_t* inverse_order) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t tok = original[packed[i / bs] * bs + i % bs];
+    order[i] = tok;
+    inverse_order[tok] = i;
+  }
+}
+
+__global__ void zero_kernel(uint32_t* p, int64_t words) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < words; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0;
+}
+
+__device__ __forceinline__ int tile_label(int64_t pos, int64_t off, int64_t n, int64_t width) {
+  return (int)((((pos - off) % n) + n) % n / width);
+}
+
+// scores[qa*nb + qc] += 1 and [qc*nb + qa] += 1 for every 4-neighbour raster pair (a, c) whose
+// tokens carry different tile labels; qa, qc are original block ids (bridge_k.py:22-28).
+__global__ void scores_kernel(int g, int bs, int64_t off, int64_t width, const int64_t* inverse,
+                              int32_t* scores) {
+  const int64_t n = (int64_t)g * g;
+  const int nb = (int)(n / bs);
+  const int64_t pairs = 2 * (int64_t)g * (g - 1);
+  for (int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; p < pairs; p += (int64_t)gridDim.x * blockDim.x) {
+    int64_t a, c;
+    if (p < (int64_t)g * (g - 1)) {  // horizontal: (y, x) - (y, x+1)
+      const int64_t y = p / (g - 1), x = p % (g - 1);
+      a = y * g + x;
+      c = a + 1;
+    } else {  // vertical: (y, x) - (y+1, x)
+      const int64_t q = p - (int64_t)g * (g - 1);
+      a = q;
+      c = q + g;
+    }
+    const int64_t pa = inverse[a], pc = inverse[c];
+    if (tile_label(pa, off, n, width) != tile_label(pc, off, n, width)) {
+      const int ba = (int)(pa / bs), bc = (int)(pc / bs);
+      atomicAdd(&scores[(int64_t)ba * nb + bc], 1);
+      atomicAdd(&scores[(int64_t)bc * nb + ba], 1);
+    }
+  }
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t lo = __shfl_xor((unsigned)(v & 0xffffffffu), off);
+    const uint32_t hi = __shfl_xor((unsigned)(v >> 32), off);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// One wave per query block q: K rounds of "largest (score, nb-1-rolled) strictly below the last
+// pick" give the top-K by (-score, (key - offset_blocks) mod nb) (bridge_k.py:36-40).
+__global__ void topk_kernel(int nb, int k, int offset_blocks, const int32_t* scores, int64_t* chosen) {
+  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (wave >= nb) return;
+  const int q = wave;
+  uint64_t bound = ~0ull;
+  for (int j = 0; j < k; ++j) {
+    uint64_t best = 0;
+    for (int key = lane; key < nb; key += 64) {
+      const int s = scores[(int64_t)q * nb + key];
+      if (s <= 0) continue;
+      const int rolled = ((key - offset_blocks) % nb + nb) % nb;
+      const uint64_t code = ((uint64_t)(uint32_t)s << 32) | (uint32_t)(nb - 1 - rolled);
+      if (code < bound && code > best) best = code;
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) {
+      if (best) {
+        const int rolled = nb - 1 - (int)(best & 0xffffffffu);
+        chosen[(int64_t)q * k + j] = (rolled + offset_blocks) % nb;
+      } else {
+        chosen[(int64_t)q * k + j] = -1;
+      }
+    }
+    bound = best ? best : 0;  // once exhausted every later round finds nothing
+  }
+}
+
+// Base rows: word w of ordinary row r = globals (physical id < gb) | ordinary blocks whose tile
+// label equals that of the row's block (plan.py:173-183).
+__global__ void base_bits_kernel(int nq, int words, int T, int gb, int text_blocks, int bs,
+                                 int64_t off, int64_t n, int64_t width, const int64_t* packed,
+                                 uint32_t* bits) {
+  const int64_t total = (int64_t)nq * words;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * blockDim.x) {
+    const int r = (int)(idx / words), w = (int)(idx % words);
+    const int64_t o = packed[gb - text_blocks + r];
+    const int lab = tile_label(o * bs, off, n, width);
+    uint32_t word = 0;
+    for (int bit = 0; bit < 32; ++bit) {
+      const int p = w * 32 + bit;
+      if (p >= T) break;
+      bool on;
+      if (p < gb) on = true;
+      else on = tile_label(packed[p - text_blocks] * bs, off, n, width) == lab;
+      word |= (uint32_t)on << bit;
+    }
+    bits[idx] = word;
+  }
+}
+
+// Bridge bits: directed adds (phys q -> phys key) to ordinary rows; reciprocal adds both directions.
+__global__ void bridge_bits_kernel(int nb, int k, int words, int gb, int reciprocal,
+                                   const int64_t* chosen, const int64_t* to_physical, uint32_t* bits) {
+  const int64_t total = (int64_t)nb * k;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t key = chosen[idx];
+    if (key < 0) continue;
+    const int pq = (int)to_physical[idx / k];
+    const int pk = (int)to_physical[key];
+    if (pq >= gb) atomicOr(&bits[(int64_t)(pq - gb) * words + pk / 32], 1u << (pk % 32));
+    if (reciprocal && pk >= gb) atomicOr(&bits[(int64_t)(pk - gb) * words + pq / 32], 1u << (pq % 32));
+  }
+}
+
+// Existing unpaired tables -> bits (used to pair arbitrary validated tables).
+__global__ void table_bits_kernel(const int32_t* ids, const int32_t* counts, int rows, int width,
+                                  int words, int T, uint32_t* bits) {
+  const int64_t total = (int64_t)rows * width;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * blockDim.x) {
+    const int r = (int)(idx / width), e = (int)(idx % width);
+    if (e >= counts[r]) continue;
+    const int p = ids[idx];
+    if (p < 0 || p >= T) continue;  // tables are validated on the host; never write out of range
+    atomicOr(&bits[(int64_t)r * words + p / 32], 1u << (p % 32));
+  }
+}
+
+// Merged word of paired row pr for key-block granularity ratio (1: 64-token keys, 2: 128-token):
+// returns the union mask over key blocks covered by 32*ratio physical ids starting at word w*ratio,
+// computed lazily per key block below.
+__device__ __forceinline__ int pair_flag(const uint32_t* ra, const uint32_t* rb, int kb, int ratio) {
+  int flag = 0;
+  for (int kh = 0; kh < ratio; ++kh) {
+    const int p = kb * ratio + kh;
+    const uint32_t a = (ra[p / 32] >> (p % 32)) & 1u;
+    const uint32_t b = (rb[p / 32] >> (p % 32)) & 1u;
+    flag |= (int)(a << (2 * kh)) | (int)(b << (1 + 2 * kh));
+  }
+  return flag;
+}
+
+// Counts: one wave per row.  mode 0: unpaired rows (popcount); mode 1: paired rows at ratio.
+// max_counts[mode] receives the widest row (atomicMax).
+__global__ void count_kernel(const uint32_t* bits, int rows_out, int words, int T, int mode, int ratio,
+                             int32_t* counts, int32_t* max_counts) {
+  const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (row >= rows_out) return;
+  int c = 0;
+  if (mode == 0) {
+    const uint32_t* r = bits + (int64_t)row * words;
+    for (int w = lane; w < words; w += 64) c += __popc(r[w]);
+  } else {
+    const uint32_t* ra = bits + (int64_t)(2 * row) * words;
+    const uint32_t* rb = ra + words;
+    const int kblocks = (T + ratio - 1) / ratio;
+    for (int kb = lane; kb < kblocks; kb += 64) c += pair_flag(ra, rb, kb, ratio) != 0;
+  }
+  for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off);
+  if (lane == 0) {
+    counts[row] = c;
+    atomicMax(&max_counts[mode], c);
+  }
+}
+
+// Emit ascending ids (and flags) of each row, zero padded to `width`; one wave per row walking
+// 64 key blocks per step with a ballot-based prefix.
+__global__ void emit_kernel(const uint32_t* bits, int rows_out, int words, int T, int mode, int ratio,
+                            int32_t* ids, int32_t* flags, int width) {
+  const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (row >= rows_out) return;
+  const uint32_t* ra = bits + (int64_t)(mode ? 2 * row : row) * words;
+  const uint32_t* rb = ra + words;
+  const int kblocks = mode ? (T + ratio - 1) / ratio : T;
+  int base = 0;
+  for (int k0 = 0; k0 < kblocks; k0 += 64) {
+    const int kb = k0 + lane;
+    int flag = 0;
+    if (kb < kblocks) {
+      if (mode) flag = pair_flag(ra, rb, kb, ratio);
+      else flag = (int)((ra[kb / 32] >> (kb % 32)) & 1u);
+    }
+    const uint64_t ballot = __ballot(flag != 0);
+    const int before = __popcll(ballot & ((1ull << lane) - 1ull));
+    if (flag && base + before < width) {
+      ids[(int64_t)row * width + base + before] = kb;
+      if (flags) flags[(int64_t)row * width + base + before] = flag;
+    }
+    base += __popcll(ballot);
+  }
+  for (int e = base + lane; e < width; e += 64) {
+    ids[(int64_t)row * width + e] = 0;
+    if (flags) flags[(int64_t)row * width + e] = 0;
+  }
+}
+
+int grid_for(int64_t work) {
+  int64_t g = (work + TPB - 1) / TPB;
+  if (g > 65536) g = 65536;
+  return g < 1 ? 1 : (int)g;
+}
+
+}  // namespace
+}  // namespace hb
+
+using namespace hb;
+
+extern "C" int hb_hilbert_order(int32_t grid_size, int64_t* out, hb_stream_t stream) {
+  HB_REQUIRE(grid_size >= 2 && (grid_size & (grid_size - 1)) == 0,
+             "Hilbert grid side must be a power of two >= 2");
+  HB_REQUIRE(out, "null output");
+  const int64_t n = (int64_t)grid_size * grid_size;
+  hipLaunchKernelGGL(hilbert_kernel, dim3(grid_for(n)), dim3(TPB), 0, stream, grid_size, out);
+  HB_HIP(hipGetLastError());
+  return HB_OK;
+}
+
+extern "C" int hb_plan_layout(int32_t grid_size, int32_t block_size, int32_t text_tokens,
+                              int32_t shared, int64_t* original_order, int64_t* inverse_original,
+                              int64_t* image_order, int64_t* inverse_image_order,
+                              int64_t* physical_original_blocks, int64_t* original_to_physical,
+                              int32_t* status, hb_stream_t stream) {
+  HB_REQUIRE(grid_size >= 8 && (grid_size & (grid_size - 1)) == 0,
+             "grid_size must be a power of two >= 8");
+  HB_REQUIRE(block_size > 0 && text_tokens > 0 && text_tokens % block_size == 0,
+             "text prefix must be block aligned");
+  const int64_t n = (int64_t)grid_size * grid_size;
+  HB_REQUIRE(n % block_size == 0 && n / block_size <= (1 << 20), "image tokens must be whole blocks");
+  HB_REQUIRE(original_order && inverse_original && image_order && inverse_image_order &&
+                 physical_original_blocks && original_to_physical && status,
+             "null output");
+  hipLaunchKernelGGL(composite_kernel, dim3(grid_for(n)), dim3(TPB), 0, stream, grid_size,
+                     original_order, inverse_original);
+  hipLaunchKernelGGL(pack_blocks_kernel, dim3(1), dim3(1024), 0, stream, grid_size, block_size,
+                     shared, (const int64_t*)original_order, text_tokens / block_size,
+                     physical_original_blocks, original_to_physical, status);
+  hipLaunchKernelGGL(image_order_kernel, dim3(grid_for(n)), dim3(TPB), 0, stream, n, block_size,
+                     (const int64_t*)original_order, (const int64_t*)physical_original_blocks,
+                     image_order, inverse_image_order);
+  HB_HIP(hipGetLastError());
+  return HB_OK;
+}
+
+extern "C" int64_t hb_plan_scratch_bytes(int32_t grid_size, int32_t block_size) {
+  if (grid_size <= 0 || block_size <= 0) return -1;
+  const int64_t nb = (int64_t)grid_size * grid_size / block_size;
+  return nb * nb * 4;
+}
+
+extern "C" int hb_plan_phase_bits(const int64_t* inverse_original,
+                                  const int64_t* physical_original_blocks,
+                                  const int64_t* original_to_physical, int32_t grid_size,
+                                  int32_t tile_count, int32_t text_tokens, int32_t block_size,
+                                  int32_t shared_blocks, int32_t phase, int32_t bridge_mode,
+                                  int32_t k, int32_t* scores, int64_t* bridge_original_blocks,
+                                  uint32_t* bits, hb_stream_t stream) {
+  const int64_t n = (int64_t)grid_size * grid_size;
+  HB_REQUIRE(grid_size >= 8 && tile_count > 0 && block_size > 0, "invalid plan geometry");
+  HB_REQUIRE(n % tile_count == 0 && (n / tile_count) % (4 * block_size) == 0 &&
+                 text_tokens % block_size == 0,
+             "Tile quarter offsets and text prefix must be block aligned");
+  HB_REQUIRE(phase >= 0 && phase < 4, "phase must be 0..3");
+  HB_REQUIRE(bridge_mode >= 0 && bridge_mode <= 2, "bridge_mode must be 0 (none), 1 (directed), 2 (reciprocal)");
+  HB_REQUIRE(bridge_mode == 0 || (k >= 1 && k <= 4), "bridge K must be 1..4");
+  HB_REQUIRE(inverse_original && physical_original_blocks && original_to_physical && bits, "null pointer");
+  HB_REQUIRE(bridge_mode == 0 || (scores && bridge_original_blocks), "bridges need scores and chosen buffers");
+  const int nb = (int)(n / block_size);
+  const int text_blocks = text_tokens / block_size;
+  const int T = text_blocks + nb;
+  const int gb = text_blocks + shared_blocks;
+  const int nq = T - gb;
+  const int words = (T + 31) / 32;
+  const int64_t width = n / tile_count;
+  const int64_t off = phase * (width / 4);
+  hipLaunchKernelGGL(base_bits_kernel, dim3(grid_for((int64_t)nq * words)), dim3(TPB), 0, stream, nq,
+                     words, T, gb, text_blocks, block_size, off, n, width, physical_original_blocks,
+                     bits);
+  if (bridge_mode) {
+    hipLaunchKernelGGL(zero_kernel, dim3(grid_for((int64_t)nb * nb)), dim3(TPB), 0, stream,
+                       (uint32_t*)scores, (int64_t)nb * nb);
+    hipLaunchKernelGGL(scores_kernel, dim3(grid_for(2 * n)), dim3(TPB), 0, stream, grid_size,
+                       block_size, off, width, inverse_original, scores);
+    hipLaunchKernelGGL(topk_kernel, dim3((nb * 64 + TPB - 1) / TPB), dim3(TPB), 0, stream, nb, k,
+                       (int)(off / block_size), (const int32_t*)scores, bridge_original_blocks);
+    hipLaunchKernelGGL(bridge_bits_kernel, dim3(grid_for((int64_t)nb * k)), dim3(TPB), 0, stream, nb,
+                       k, words, gb, bridge_mode == 2, (const int64_t*)bridge_original_blocks,
+                       original_to_physical, bits);
+  }
+  HB_HIP(hipGetLastError());
+  return HB_OK;
+}
+
+extern "C" int hb_table_bits(const int32_t* kv_indices, const int32_t* kv_counts, int32_t rows,
+                             int32_t width, int32_t total_blocks, uint32_t* bits,
+                             hb_stream_t stream) {
+  HB_REQUIRE(kv_indices && kv_counts && bits && rows > 0 && width > 0 && total_blocks > 0,
+             "invalid table arguments");
+  const int words = (total_blocks + 31) / 32;
+  hipLaunchKernelGGL(zero_kernel, dim3(grid_for((int64_t)rows * words)), dim3(TPB), 0, stream, bits,
+                     (int64_t)rows * words);
+  hipLaunchKernelGGL(table_bits_kernel, dim3(grid_for((int64_t)rows * width)), dim3(TPB), 0, stream,
+                     kv_indices, kv_counts, rows, width, words, total_blocks, bits);
+  HB_HIP(hipGetLastError());
+  return HB_OK;
+}
+
+extern "C" int hb_bits_counts(const uint32_t* bits, int32_t rows, int32_t total_blocks,
+                              int32_t key_block_size, int32_t* counts, int32_t* paired_counts,
+                              int32_t* max_counts, hb_stream_t stream) {
+  HB_REQUIRE(bits && max_counts && rows > 0 && total_blocks > 0, "invalid bitmap arguments");
+  HB_REQUIRE(key_block_size == 64 || key_block_size == 128, "key_block_size must be 64 or 128");
+  HB_REQUIRE(!paired_counts || rows % 2 == 0, "paired rows need an even row count");
+  const int words = (total_blocks + 31) / 32;
+  hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(64), 0, stream, (uint32_t*)max_counts, (int64_t)2);
+  if (counts)
+    hipLaunchKernelGGL(count_kernel, dim3((rows * 64 + TPB - 1) / TPB), dim3(TPB), 0, stream, bits, rows,
+                       words, total_blocks, 0, 1, counts, max_counts);
+  if (paired_counts)
+    hipLaunchKernelGGL(count_kernel, dim3((rows / 2 * 64 + TPB - 1) / TPB), dim3(TPB), 0, stream, bits,
+                       rows / 2, words, total_blocks, 1, key_block_size / 64, paired_counts, max_counts);
+  HB_HIP(hipGetLastError());
+  return HB_OK;
+}
+
+extern "C" int hb_bits_emit(const uint32_t* bits, int32_t rows, int32_t total_blocks,
+                            int32_t key_block_size, int32_t* ids, int32_t width, int32_t* paired_ids,
+                            int32_t* paired_flags, int32_t paired_width, hb_stream_t stream) {
+  HB_REQUIRE(bits && rows > 0 && total_blocks > 0, "invalid bitmap arguments");
+  HB_REQUIRE(key_block_size == 64 || key_block_size == 128, "key_block_size must be 64 or 128");
+  const int words = (total_blocks + 31) / 32;
+  if (ids) {
+    HB_REQUIRE(width > 0, "width must be positive");
+    hipLaunchKernelGGL(emit_kernel, dim3((rows * 64 + TPB - 1) / TPB), dim3(TPB), 0, stream, bits, rows,
+                       words, total_blocks, 0, 1, ids, (int32_t*)nullptr, width);
+  }
+  if (paired_ids) {
+    HB_REQUIRE(paired_flags && paired_width > 0 && rows % 2 == 0, "paired output needs flags and width");
+    hipLaunchKernelGGL(emit_kernel, dim3((rows / 2 * 64 + TPB - 1) / TPB), dim3(TPB), 0, stream, bits,
+                       rows / 2, words, total_blocks, 1, key_block_size / 64, paired_ids, paired_flags,
+                       paired_width);
+  }
+  HB_HIP(hipGetLastError());
+  return HB_OK;
+}

@@ -16,6 +16,7 @@ from dataclasses import dataclass, replace
 import torch
 
 from . import _lib
+from ._tables import emit_device, table_bits_device
 from .sparse_kernel import validate_metadata
 
 
@@ -40,26 +41,15 @@ class PairedMetadata:
 def pair_tables_device(kv_indices, kv_counts, *, tokens, key_block_size):
     """Pair validated int32 tables already on the GPU; returns (ids, flags, counts) on the GPU.
 
-    One host synchronisation reads the widest paired row, which fixes the table width.
+    The rows become adjacency bitmaps (hb_table_bits), paired rows are emitted in ascending key
+    block order (hb_bits_counts / hb_bits_emit).  One host synchronisation reads the widest paired
+    row, which fixes the table width.
     """
     _lib.require_gpu(kv_indices, kv_counts)
-    lib = _lib.load()
-    rows, width = kv_indices.shape
-    kv_indices = kv_indices.contiguous()
-    kv_counts = kv_counts.contiguous()
-    ratio = key_block_size // 64
-    cap = (tokens // 64 + ratio - 1) // ratio
-    dev = kv_indices.device
-    ids = torch.empty((rows // 2, cap), dtype=torch.int32, device=dev)
-    flags = torch.empty_like(ids)
-    counts = torch.empty(rows // 2, dtype=torch.int32, device=dev)
-    rc = lib.hb_pair_tables(
-        kv_indices.data_ptr(), kv_counts.data_ptr(), rows, width, tokens // 64, key_block_size,
-        ids.data_ptr(), flags.data_ptr(), counts.data_ptr(), cap, _lib.stream_ptr(dev),
-    )
-    _lib.check(rc, "hb_pair_tables")
-    out_width = max(int(counts.max()), 1)  # setup-time sync: the table width is data dependent
-    return ids[:, :out_width].contiguous(), flags[:, :out_width].contiguous(), counts
+    total_blocks = tokens // 64
+    bits = table_bits_device(kv_indices.contiguous(), kv_counts.contiguous(), total_blocks)
+    out = emit_device(bits, total_blocks, unpaired=False, paired=True, key_block_size=key_block_size)
+    return out["paired_indices"], out["paired_flags"], out["paired_counts"]
 
 
 def pair_metadata(kv_indices, kv_counts, *, tokens, global_tokens=768, key_block_size=64, device=None):

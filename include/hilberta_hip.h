@@ -68,6 +68,59 @@ int hb_block_sparse_fwd(const void* q, const void* k, const void* v, void* out, 
                         void* workspace, int64_t workspace_bytes, int32_t num_groups,
                         hb_stream_t stream);
 
+/* ---------------------------------------------------------------- (a) Hilbert permutation
+ * dst[o, i, :] = src[o, index[i], :] for o < outer, i < rows, each row row_bytes contiguous bytes
+ * (strides in bytes).  Replaces x.index_select(dim, order) of reference
+ * hilberta/flux_adapter.py:209-212 (entry), :243 (exit) and sampling_layout.py:96-97, :110.
+ * Indices outside [0, src_rows) are skipped and set *error (device int, may be NULL) to 1. */
+int hb_gather_rows(const void* src, void* dst, const int64_t* index, int64_t rows, int64_t outer,
+                   int64_t src_outer_stride, int64_t dst_outer_stride, int64_t src_row_stride,
+                   int64_t dst_row_stride, int64_t row_bytes, int64_t src_rows, int32_t* error,
+                   hb_stream_t stream);
+
+/* ---------------------------------------------------------------- (b) block tables
+ * Hilbert order of a grid_size x grid_size raster (reference hilberta/geometry.py:6-25). */
+int hb_hilbert_order(int32_t grid_size, int64_t* out, hb_stream_t stream);
+
+/* Composite order and physical packing (reference hilberta/plan.py:133-150, :186-197):
+ * original_order / inverse_original [n], image_order / inverse_image_order [n],
+ * physical_original_blocks [nb] (shared blocks first) and original_to_physical [nb] (+ text
+ * blocks).  status (device int32[2]) receives {#shared blocks, partial-shared-block flag}. */
+int hb_plan_layout(int32_t grid_size, int32_t block_size, int32_t text_tokens, int32_t shared,
+                   int64_t* original_order, int64_t* inverse_original, int64_t* image_order,
+                   int64_t* inverse_image_order, int64_t* physical_original_blocks,
+                   int64_t* original_to_physical, int32_t* status, hb_stream_t stream);
+
+/* Scratch bytes for the bridge score matrix of one phase (nb * nb int32). */
+int64_t hb_plan_scratch_bytes(int32_t grid_size, int32_t block_size);
+
+/* Adjacency bitmap of one phase: bits [ordinary rows][ceil(T/32)] uint32.  Rows hold the global
+ * prefix and the same-tile ordinary blocks (plan.py:153-184); bridge_mode 1 adds the directed
+ * top-1 bridge of build_plan (plan.py:159-172), 2 the reciprocal top-K of bridge_k_plan
+ * (bridge_k.py:21-44).  bridge_original_blocks [nb, k] int64 receives the chosen key blocks
+ * (-1 = none); scores is nb*nb int32 scratch. */
+int hb_plan_phase_bits(const int64_t* inverse_original, const int64_t* physical_original_blocks,
+                       const int64_t* original_to_physical, int32_t grid_size, int32_t tile_count,
+                       int32_t text_tokens, int32_t block_size, int32_t shared_blocks,
+                       int32_t phase, int32_t bridge_mode, int32_t k, int32_t* scores,
+                       int64_t* bridge_original_blocks, uint32_t* bits, hb_stream_t stream);
+
+/* Bitmap of existing unpaired tables (rows x width ids with counts), for pairing them. */
+int hb_table_bits(const int32_t* kv_indices, const int32_t* kv_counts, int32_t rows, int32_t width,
+                  int32_t total_blocks, uint32_t* bits, hb_stream_t stream);
+
+/* Row lengths of a bitmap: unpaired counts [rows] and/or paired counts [rows/2] at
+ * key_block_size 64 or 128; max_counts (device int32[2]) receives the widest of each. */
+int hb_bits_counts(const uint32_t* bits, int32_t rows, int32_t total_blocks,
+                   int32_t key_block_size, int32_t* counts, int32_t* paired_counts,
+                   int32_t* max_counts, hb_stream_t stream);
+
+/* Ascending, zero-padded tables from a bitmap: unpaired ids [rows, width] and/or paired ids and
+ * flags [rows/2, paired_width] with flag bit (half + 2*key_half) (paired_metadata.py:38-51). */
+int hb_bits_emit(const uint32_t* bits, int32_t rows, int32_t total_blocks, int32_t key_block_size,
+                 int32_t* ids, int32_t width, int32_t* paired_ids, int32_t* paired_flags,
+                 int32_t paired_width, hb_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

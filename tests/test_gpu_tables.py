@@ -1,0 +1,178 @@
+"""GPU: the HIP table builder and permutation gather are bit-exact against the CPU oracle / torch."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import topology as T
+from tests.helpers import say
+
+pytestmark = pytest.mark.gpu
+
+
+def _eq(a, b, what):
+    a = a.cpu().numpy() if isinstance(a, torch.Tensor) else np.asarray(a)
+    b = np.asarray(b)
+    assert a.shape == b.shape, f"{what}: shape {a.shape} != {b.shape}"
+    assert a.dtype == b.dtype or (a.dtype.kind == b.dtype.kind == "i"), f"{what}: dtype {a.dtype} {b.dtype}"
+    assert np.array_equal(a, b), f"{what}: values differ at {np.argwhere(a != b)[:5].tolist()}"
+
+
+def _plan_eq(dev, ref, what, directed):
+    assert dev.grid_size == ref["grid_size"] and dev.tile_count == ref["tile_count"]
+    assert dev.shared_tokens == ref["shared_tokens"] and dev.global_tokens == ref["global_tokens"]
+    for f in ("image_order", "inverse_image_order", "original_order", "physical_original_blocks"):
+        _eq(getattr(dev, f), ref[f], f"{what} {f}")
+        assert getattr(dev, f).dtype == torch.int64
+    for i, (p, r) in enumerate(zip(dev.phases, ref["phases"])):
+        assert p.offset == r["offset"]
+        assert p.kv_indices.dtype == torch.int32 and p.kv_counts.dtype == torch.int32
+        _eq(p.kv_indices, r["kv_indices"], f"{what} phase {i} kv_indices")
+        _eq(p.kv_counts, r["kv_counts"], f"{what} phase {i} kv_counts")
+        _eq(p.bridge_original_blocks, r["bridge_original_blocks"], f"{what} phase {i} bridges")
+
+
+@pytest.mark.parametrize("grid", [2, 4, 8, 64, 128, 256])
+def test_hilbert_order(hip_device, grid):
+    from hilberta_amd.geometry import hilbert_order
+
+    _eq(hilbert_order(grid, device=hip_device), T.hilbert_order(grid), f"hilbert {grid}")
+
+
+@pytest.mark.parametrize("grid,block,text", [(16, 4, 16), (64, 64, 512)])
+@pytest.mark.parametrize("tiles", [4, 16])
+@pytest.mark.parametrize("shared", [False, True])
+@pytest.mark.parametrize("bridge", [False, True])
+def test_build_plan_bit_exact(hip_device, grid, block, text, tiles, shared, bridge):
+    from hilberta_amd.plan import build_plan
+
+    say(f"case build_plan grid={grid} block={block} tiles={tiles} shared={shared} bridge={bridge}")
+    dev = build_plan(tiles, grid, text, shared, bridge, block, device=hip_device)
+    ref = T.build_plan(tiles, grid, text, shared, bridge, block)
+    _plan_eq(dev, ref, "build_plan", directed=True)
+
+
+@pytest.mark.parametrize("grid", [64, 128, 256])
+@pytest.mark.parametrize("tiles", [4, 16])
+@pytest.mark.parametrize("k", [1, 2, 3, 4])
+def test_bridge_k_plan_bit_exact(hip_device, grid, tiles, k):
+    from hilberta_amd.bridge_k import bridge_k_plan
+
+    say(f"case bridge_k grid={grid} tiles={tiles} k={k}")
+    dev = bridge_k_plan(tiles, k, False, grid_size=grid, device=hip_device)
+    ref = T.bridge_k_plan(tiles, k, False, grid_size=grid)
+    _plan_eq(dev, ref, f"bridge_k g{grid} t{tiles} k{k}", directed=False)
+
+
+@pytest.mark.parametrize("tiles", [4, 16])
+def test_bridge_k_shared_bit_exact(hip_device, tiles):
+    from hilberta_amd.bridge_k import bridge_k_plan
+
+    dev = bridge_k_plan(tiles, 2, True, grid_size=64, device=hip_device)
+    ref = T.bridge_k_plan(tiles, 2, True, grid_size=64)
+    _plan_eq(dev, ref, "bridge_k shared", directed=False)
+
+
+def test_pair_metadata_hand_vector(hip_device):
+    from hilberta_amd.paired_metadata import pair_metadata, unpair_metadata
+
+    ids = torch.tensor([[0, 1, 2, 4], [0, 1, 3, 5], [0, 1, 4, 5], [0, 1, 4, 5]], dtype=torch.int32)
+    counts = torch.full((4,), 4, dtype=torch.int32)
+    meta = pair_metadata(ids, counts, tokens=384, global_tokens=128, key_block_size=128,
+                         device=hip_device)
+    assert meta.kv_indices[0, :3].tolist() == [0, 1, 2]
+    assert meta.kv_flags[0, :3].tolist() == [15, 9, 9]
+    assert unpair_metadata(meta) == ids.tolist()
+
+
+@pytest.mark.parametrize("name,grid,tiles,k", [("1024_t4k1", 64, 4, 1), ("1024_t16k3", 64, 16, 3),
+                                               ("2048_t16k3", 128, 16, 3), ("4096_t16k3", 256, 16, 3)])
+@pytest.mark.parametrize("key_block", [64, 128])
+def test_pair_metadata_bit_exact(hip_device, name, grid, tiles, k, key_block):
+    from hilberta_amd.paired_metadata import pair_metadata
+
+    ref_plan = T.bridge_k_plan(tiles, k, False, grid_size=grid)
+    for phase in range(4):
+        say(f"case pair_metadata {name} phase {phase} KB{key_block}")
+        p = ref_plan["phases"][phase]
+        ref = T.pair_metadata(p["kv_indices"], p["kv_counts"], tokens=ref_plan["total_tokens"],
+                              global_tokens=ref_plan["global_tokens"], key_block_size=key_block)
+        meta = pair_metadata(torch.from_numpy(p["kv_indices"]), torch.from_numpy(p["kv_counts"]),
+                             tokens=ref_plan["total_tokens"], global_tokens=ref_plan["global_tokens"],
+                             key_block_size=key_block, device=hip_device)
+        for f in ("kv_indices", "kv_flags", "kv_counts"):
+            _eq(getattr(meta, f), ref[f], f"{name} phase {phase} {f}")
+
+
+@pytest.mark.parametrize("grid,tiles,k", [(64, 4, 1), (128, 16, 3), (256, 16, 3)])
+def test_paired_plan_device_bit_exact(hip_device, grid, tiles, k):
+    from hilberta_amd.bridge_k import paired_plan_device
+
+    dp = paired_plan_device(tiles, k, grid_size=grid, device=hip_device)
+    ref_plan = T.bridge_k_plan(tiles, k, False, grid_size=grid)
+    _eq(dp.layout.image_order, ref_plan["image_order"], "image_order")
+    for phase, meta in enumerate(dp.phases):
+        p = ref_plan["phases"][phase]
+        ref = T.pair_metadata(p["kv_indices"], p["kv_counts"], tokens=ref_plan["total_tokens"],
+                              global_tokens=ref_plan["global_tokens"])
+        assert meta.tokens == ref_plan["total_tokens"] and meta.global_tokens == 512
+        for f in ("kv_indices", "kv_flags", "kv_counts"):
+            _eq(getattr(meta, f), ref[f], f"device plan phase {phase} {f}")
+
+
+# ---------------------------------------------------------------------------- permutation
+@pytest.mark.parametrize(
+    "shape,dim,dtype",
+    [
+        ((1, 4096, 64), 1, torch.bfloat16),  # 1024 px latents
+        ((2, 16384, 64), 1, torch.bfloat16),  # 2048 px latents, B=2
+        ((4096, 3), 0, torch.float32),  # position ids (12-byte rows)
+        ((2, 4096, 3), 1, torch.int64),  # batched ids (24-byte rows)
+        ((1, 4608, 3072), 1, torch.bfloat16),  # hidden states
+        ((1, 4608, 24, 128), 1, torch.bfloat16),  # BNHD projections
+        ((3, 1000, 7), 1, torch.uint8),  # odd byte rows
+    ],
+)
+def test_index_select_rows_bit_exact(hip_device, shape, dim, dtype):
+    from hilberta_amd.layout import index_select_rows
+
+    gen = torch.Generator("cpu").manual_seed(7)
+    if dtype.is_floating_point:
+        x = torch.randn(shape, generator=gen).to(dtype)
+    else:
+        x = torch.randint(0, 100, shape, generator=gen).to(dtype)
+    x = x.to(hip_device)
+    index = torch.randperm(shape[dim], generator=gen).to(hip_device)
+    out = index_select_rows(x, dim, index)
+    assert torch.equal(out, x.index_select(dim, index))
+    inv = torch.empty_like(index)
+    inv[index] = torch.arange(len(index), device=hip_device)
+    assert torch.equal(index_select_rows(out, dim, inv), x)  # unpermute round trip
+
+
+def test_index_select_rows_strided_and_errors(hip_device):
+    from hilberta_amd.layout import index_select_rows
+
+    x = torch.randn(2, 512, 24, 128, device=hip_device).to(torch.bfloat16)
+    view = x.transpose(1, 2)[:, :, :, :]  # [2, 24, 512, 128], gather along the token dim 2
+    index = torch.randperm(512, device=hip_device)
+    assert torch.equal(index_select_rows(view, 2, index), view.index_select(2, index))
+    err = torch.zeros((), dtype=torch.int32, device=hip_device)
+    bad = index.clone()
+    bad[5] = 512
+    index_select_rows(x, 1, bad, error=err)
+    assert int(err) == 1
+    with pytest.raises(ValueError):
+        index_select_rows(x.transpose(2, 3), 1, index)  # row not contiguous
+
+
+def test_plan_layout_permutes_latents(hip_device):
+    """Permute at entry, unpermute at exit with the device plan's orders (sampling_layout.py:88-116)."""
+    from hilberta_amd.bridge_k import paired_plan_device
+    from hilberta_amd.layout import permute_tokens, unpermute_tokens
+
+    dp = paired_plan_device(16, 3, grid_size=128, device=hip_device)
+    lat = torch.randn(1, 16384, 64, device=hip_device).to(torch.bfloat16)
+    packed = permute_tokens(lat, dp.layout.image_order)
+    assert torch.equal(packed, lat.index_select(1, dp.layout.image_order))
+    assert torch.equal(unpermute_tokens(packed, dp.layout.inverse_image_order), lat)
