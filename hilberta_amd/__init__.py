@@ -1,0 +1,20 @@
+"""HilbertA inference attention path for AMD Instinct MI355X (gfx950).
+
+Composite-Hilbert token layout, sliding tiles and reciprocal block bridges (wenboluu/hilberta),
+rebuilt on hand-written HIP kernels behind a C ABI (include/hilberta_hip.h):
+
+  layout            Hilbert permute / unpermute of token rows (HIP gather)
+  geometry / plan / bridge_k / paired_metadata
+                    block tables built on the GPU, bit-exact with the reference
+  paired_kernel / sparse_kernel
+                    block-sparse flash-attention forward (bf16/fp16 MFMA, persistent)
+
+The modules keep the reference package's call surface.  There is no CPU fallback: the HIP library
+(python -m hilberta_amd.build) and a GPU are required for every computation.
+"""
+
+from .bridge_k import bridge_k_plan
+
+__version__ = "0.1.0"
+
+__all__ = ["bridge_k_plan"]
