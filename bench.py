@@ -113,6 +113,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="attention only (for counter runs)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only copy MIB MiB device-to-device 5 times (calibrates FETCH/WRITE_SIZE)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py runs on one GPU: --gpus {a.gpus} is not supported in this build "
@@ -121,6 +123,15 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+
+    if a.copy_probe:
+        x = torch.ones(a.copy_probe << 20, dtype=torch.uint8, device="cuda:0")
+        y = torch.empty_like(x)
+        for _ in range(5):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": x.numel(), "copies": 5}))
+        return
 
     from hilberta_amd.bridge_k import paired_plan_device
     from hilberta_amd.paired_kernel import paired_attention

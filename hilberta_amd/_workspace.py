@@ -1,8 +1,8 @@
 """Per-(device, stream) workspaces for the attention kernels.
 
-A workspace holds the persistent kernel's queue counters (which the kernel resets itself when
-it finishes, so a buffer is zero-filled only once, at allocation) and the partials of split
-global query tiles.  Keying by stream keeps launches that may overlap from sharing counters.
+A workspace holds the persistent kernel's work-queue counters (zero-filled once at allocation;
+every launch leaves them at zero) and the partial results of split global query tiles.  Keying
+by stream keeps launches that may overlap in time from sharing one.
 """
 
 from __future__ import annotations

@@ -5,13 +5,14 @@
 //
 //  * Work item = one query tile (128 queries for paired tables, 64 for unpaired ones) of one
 //    (batch, head), or one chunk of a global (text) query tile's all-key sweep.  Global tiles are
-//    split into chunks of about one table row's length so no item is longer than the longest
-//    ordinary row; chunk partials (unnormalised accumulator, running max, row sum) are merged by
-//    the last chunk to finish (counter in the workspace).
-//  * Persistent workgroups (2 per CU) pull items from 8 queues, one per XCD, each queue owning the
-//    heads bh = q, q+8, ...; a workgroup starts with the queue of its own XCD (dispatch is round
-//    robin over XCDs) so items that share K/V blocks run under one L2, then steals from the
-//    others.  Queue heads reset themselves when the last workgroup leaves.
+//    split into at most 4 chunks, none shorter than the longest ordinary row, so no item
+//    dominates the schedule; chunk partials (unnormalised accumulator, running max, row sum) go to
+//    the workspace and merge_kernel combines them after the main kernel.
+//  * Persistent workgroups (2 per CU) claim items from 8 work queues, one per XCD (queue x =
+//    blockIdx % 8, the XCD under round-robin dispatch, owns a contiguous range of the item list),
+//    so items that share K/V blocks run under one L2; idle workgroups steal from other queues.
+//    Claims run one item ahead, and the next item's table entries, first K/V block and Q tile are
+//    prefetched while the current item finishes, so no claim or load latency sits between items.
 //  * Per 64-key block: K (row major) and V (transposed, keys permuted to the MFMA operand order)
 //    are staged through double-buffered LDS; the next block's global loads are in flight while the
 //    current block is computed.  Blocks whose flags allow neither query half are never loaded.
@@ -32,13 +33,13 @@ namespace hb {
 namespace {
 
 constexpr int KEYS = 64;     // keys per staged block
-constexpr int PAD = 8;       // LDS row padding in elements (16 bytes) against bank conflicts
 constexpr float LN2 = 0.69314718055994530942f;
 constexpr int QUEUES = 8;    // one work queue per XCD
-// The workspace starts with a fixed counter region (queue heads, exit count, one merge counter
-// per split global tile) that every launch leaves at zero, whatever its shapes; partials follow.
-constexpr int64_t COUNTER_BYTES = 64 * 1024;
-constexpr int64_t MAX_SPLIT_TILES = COUNTER_BYTES / 4 - 16;
+constexpr float RESCALE_LOG2 = 8.0f;  // lazy-rescale threshold (log2 units)
+constexpr int MAX_SPLIT = 16;         // chunks per global query tile
+// __builtin_amdgcn_sched_group_barrier instruction classes
+constexpr int SG_MFMA = 0x008;
+constexpr int SG_DS_READ = 0x100;
 
 struct AttnArgs {
   const uint16_t* q;
@@ -53,7 +54,7 @@ struct AttnArgs {
   int32_t heads, tokens, bh, width, rows, key_blocks;
   int32_t global_tiles, nsplit, chunk, per_bh;
   float scale_log2;
-  int32_t* counters;  // [0..7] queue heads, [8] exit count, [16 + tile] split-merge counters
+  int32_t* counters;  // [0, 8) queue heads, [8] exit count; zero between launches
   float* part;        // split partial accumulators, fragment order
   float* part_ml;     // split partial (max, sum) per query lane
 };
@@ -103,12 +104,37 @@ __device__ __forceinline__ float pair_sum(float x, int partner) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Position of key kappa (0..15) inside a 16-key group of the transposed V tile: the order in
-// which a lane's S^T registers present keys to the PV MFMA (lane half hl, slot r -> key
-// 8*(r/4) + 4*hl + r%4).
-__device__ __forceinline__ int vpos4(int g) {  // first position of keys 4g..4g+3, g in 0..15
-  const int k0 = (g & 3) * 4;
-  return 16 * (g >> 2) + 8 * ((k0 >> 2) & 1) + 4 * (k0 >> 3);
+// acc + (lo + hi) of a packed pair of 16-bit values (v_dot2_f32_{bf16,f16} against (1, 1)).
+template <bool F16>
+__device__ __forceinline__ float dot2_sum(uint32_t pair, float acc) {
+  if constexpr (F16) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 one = {(_Float16)1.f, (_Float16)1.f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pair), one, acc, false);
+  } else {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const b2 one = {(__bf16)1.f, (__bf16)1.f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, pair), one, acc, false);
+  }
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// Chunk permutation of K/V row r in LDS (16-byte chunks, CPR per row): XOR with a row-dependent
+// value so that the K reads (8 consecutive rows, one 16-byte chunk each) and the transposing V
+// reads (4 consecutive rows, 4 neighbouring chunks each per 32 lanes) hit distinct banks.
+template <int CPR>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (CPR == 16) return 4 * (r & 3) + ((r >> 2) & 3);
+  else return (4 * ((r >> 1) & 1) + ((r >> 2) & 3)) & 7;
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4 of the 4-element
+// (8-byte) words addressed by lanes i/4, i/4 + 4, i/4 + 8, i/4 + 12.
+__device__ __forceinline__ u32x2 read_tr(const uint16_t* p) {
+  typedef short i16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p));
 }
 
 template <int HALVES, int D, int KBR, bool F16>
@@ -116,308 +142,457 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   constexpr int WAVES = 2 * HALVES;
   constexpr int NT = 64 * WAVES;
   constexpr int QT = 64 * HALVES;               // queries per work item
-  constexpr int KS = D + PAD;                   // K tile row stride (elements)
-  constexpr int VS = KEYS + PAD;                // V^T tile row stride (elements)
-  constexpr int K_ELEMS = KEYS * KS;
-  constexpr int STAGE = K_ELEMS + D * VS;
-  constexpr int DC = D / 8;                     // 16-byte chunks per row
-  constexpr int KCH = KEYS * DC / NT;           // K chunks per thread
-  constexpr int VGROUPS = 16 * DC;              // (4 keys x 8 dims) groups per V tile
-  constexpr int VG = (VGROUPS + NT - 1) / NT;   // V groups per thread
+  constexpr int CPR = D / 8;                    // 16-byte chunks per K/V row
+  constexpr int TILE = KEYS * D;                // elements of one K (or V) tile
+  constexpr int STAGE = 2 * TILE;               // K tile then V tile
   constexpr int DT = D / 32;                    // output 32-dim tiles
   constexpr int DS = D / 16;                    // contraction steps over D
-  static_assert(KEYS * DC % NT == 0, "K staging must divide evenly");
+  constexpr int FRAG = DT * 16 * 64;            // partial accumulator floats per wave
+  static_assert(CPR % WAVES == 0 || WAVES % CPR == 0, "tile loads must split over the waves");
 
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
-  __shared__ int s_item;
-  __shared__ int s_last;
+  // Two stages of [K tile | V tile], both row-major (key rows of D elements) with the 16-byte
+  // chunks of row r permuted by chunk ^ swz(r); written by direct global->LDS loads.
+  __shared__ __attribute__((aligned(1024))) uint16_t lds0[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds1[STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave index as a provably uniform (scalar) value, so per-wave tests such as the flag check
+  // compile to branches rather than exec-masked code
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = HALVES == 2 ? (wave >> 1) : 0;
   const int ql = lane & 31;   // query (column) owned by this lane inside the wave's 32
   const int hl = lane >> 5;   // lane half: selects the 8-element k slice of MFMA operands
   const int partner = (lane ^ 32) << 2;
 
-  const int q0 = blockIdx.x % QUEUES;
-  for (int qi = 0; qi < QUEUES; ++qi) {
-    const int queue = (q0 + qi) % QUEUES;
-    const int nbh = a.bh > queue ? (a.bh - queue + QUEUES - 1) / QUEUES : 0;
-    const int nitems = nbh * a.per_bh;
-    for (;;) {
-      if (tid == 0) s_item = atomicAdd(&a.counters[queue], 1);
-      __syncthreads();
-      const int item = uniform(s_item);
-      __syncthreads();
-      if (item >= nitems) break;
-
-      // ---------------------------------------------------------------- decode the work item
-      const int bh = queue + QUEUES * (item / a.per_bh);
-      const int rem = item % a.per_bh;
-      const int b = bh / a.heads;
-      const int h = bh - b * a.heads;
-      const bool is_global = rem < a.global_tiles * a.nsplit;
-      int qfirst, row = 0, gtile = 0, split = 0, nsteps, first_block = 0;
-      if (is_global) {
-        gtile = rem / a.nsplit;
-        split = rem - gtile * a.nsplit;
-        qfirst = gtile * QT;
-        first_block = split * a.chunk;
-        nsteps = min(a.chunk, a.key_blocks - first_block);
-      } else {
-        row = rem - a.global_tiles * a.nsplit;
-        qfirst = a.tokens - (a.rows - row) * QT;  // ordinary rows follow the global prefix
-        nsteps = a.counts[row] * KBR;
-      }
-      const int32_t* trow_ids = a.indices + (int64_t)row * a.width;
-      const int32_t* trow_flags = a.flags + (int64_t)row * a.width;
-
-      // 64-key block index and per-half permission bits of step s (bit h = query half h may see it)
-      auto step_info = [&](int s, int& kb, int& fl) {
-        if (is_global) {
-          kb = first_block + s;
-          fl = 3;
-        } else if (HALVES == 2) {
-          const int e = s / KBR;
-          const int sub = s - e * KBR;
-          kb = trow_ids[e] * KBR + sub;
-          fl = (trow_flags[e] >> (2 * sub)) & 3;
-        } else {
-          kb = trow_ids[s];
-          fl = 1;
-        }
-      };
-      auto next_live = [&](int s) {
-        for (; s < nsteps; ++s) {
-          int kb, fl;
-          step_info(s, kb, fl);
-          if (fl) break;
-        }
-        return s;
-      };
-
-      const uint16_t* kbh = a.k + b * a.k_sb + h * a.k_sh;
-      const uint16_t* vbh = a.v + b * a.v_sb + h * a.v_sh;
-
-      // ---------------------------------------------------------------- Q^T operand in registers
-      u32x4 qreg[DS];
-      {
-        const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh +
-                             (int64_t)(qfirst + wave * 32 + ql) * a.q_sn + hl * 8;
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) qreg[ds] = *(const u32x4*)(qp + ds * 16);
-      }
-
-      f32x16 acc[DT];
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
-      float m_run = -__builtin_inff();
-      float l_run = 0.f;
-
-      u32x4 kst[KCH];
-      u32x4 vst[VG][4];
-      auto load_block = [&](int kb) {
-        const uint16_t* kp = kbh + (int64_t)kb * KEYS * a.k_sn;
-        const uint16_t* vp = vbh + (int64_t)kb * KEYS * a.v_sn;
-#pragma unroll
-        for (int j = 0; j < KCH; ++j) {
-          const int idx = tid + j * NT;
-          const int r = idx / DC, c = idx % DC;
-          kst[j] = *(const u32x4*)(kp + r * a.k_sn + c * 8);
-        }
-#pragma unroll
-        for (int j = 0; j < VG; ++j) {
-          const int idx = tid + j * NT;
-          if (VGROUPS % NT == 0 || idx < VGROUPS) {
-            const int g = idx % 16, c = idx / 16;
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
-              vst[j][kk] = *(const u32x4*)(vp + (4 * g + kk) * a.v_sn + c * 8);
-          }
-        }
-      };
-      auto store_block = [&](uint16_t* stage) {
-#pragma unroll
-        for (int j = 0; j < KCH; ++j) {
-          const int idx = tid + j * NT;
-          const int r = idx / DC, c = idx % DC;
-          *(u32x4*)(stage + r * KS + c * 8) = kst[j];
-        }
-        uint16_t* vt = stage + K_ELEMS;
-#pragma unroll
-        for (int j = 0; j < VG; ++j) {
-          const int idx = tid + j * NT;
-          if (VGROUPS % NT == 0 || idx < VGROUPS) {
-            const int g = idx % 16, c = idx / 16;
-            uint16_t* dst = vt + (c * 8) * VS + vpos4(g);
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {  // word m of each key row holds dims 2m, 2m+1
-              const uint32_t w0 = vst[j][0][m], w1 = vst[j][1][m], w2 = vst[j][2][m], w3 = vst[j][3][m];
-              u32x2 even = {(w0 & 0xffffu) | (w1 << 16), (w2 & 0xffffu) | (w3 << 16)};
-              u32x2 odd = {(w0 >> 16) | (w1 & 0xffff0000u), (w2 >> 16) | (w3 & 0xffff0000u)};
-              *(u32x2*)(dst + (2 * m) * VS) = even;
-              *(u32x2*)(dst + (2 * m + 1) * VS) = odd;
-            }
-          }
-        }
-      };
-
-      // ---------------------------------------------------------------- main loop over key blocks
-      int s = next_live(0);
-      int buf = 0;
-      if (s < nsteps) {
-        int kb, fl;
-        step_info(s, kb, fl);
-        load_block(kb);
-      }
-      while (s < nsteps) {
-        int kb, fl;
-        step_info(s, kb, fl);
-        uint16_t* stage = lds + buf * STAGE;
-        store_block(stage);
-        __syncthreads();
-        const int sn = next_live(s + 1);
-        if (sn < nsteps) {
-          int kbn, fln;
-          step_info(sn, kbn, fln);
-          load_block(kbn);
-        }
-        if ((fl >> half) & 1) {
-          // S^T = K Q^T for two 32-key tiles
-          f32x16 s0 = f32x16{}, s1 = f32x16{};
-          const uint16_t* kl = stage + ql * KS + hl * 8;
-#pragma unroll
-          for (int ds = 0; ds < DS; ++ds) {
-            const u32x4 k0 = *(const u32x4*)(kl + ds * 16);
-            const u32x4 k1 = *(const u32x4*)(kl + 32 * KS + ds * 16);
-            s0 = mfma32<F16>(k0, qreg[ds], s0);
-            s1 = mfma32<F16>(k1, qreg[ds], s1);
-          }
-          // online softmax for query ql (this lane holds 32 of its 64 keys)
-          float mx = s0[0];
-#pragma unroll
-          for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s0[i]);
-#pragma unroll
-          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s1[i]);
-          mx = pair_max(mx, partner) * a.scale_log2;
-          const float m_new = fmaxf(m_run, mx);
-          const float alpha = fast_exp2(m_run - m_new);
-          const float neg = -m_new;
-          float lsum = 0.f;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            s0[i] = fast_exp2(__builtin_fmaf(s0[i], a.scale_log2, neg));
-            lsum += s0[i];
-          }
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            s1[i] = fast_exp2(__builtin_fmaf(s1[i], a.scale_log2, neg));
-            lsum += s1[i];
-          }
-          l_run = l_run * alpha + lsum;
-          m_run = m_new;
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
-          u32x4 pk[4];
-          pk[0] = pack8<F16>(f32x8{s0[0], s0[1], s0[2], s0[3], s0[4], s0[5], s0[6], s0[7]});
-          pk[1] = pack8<F16>(f32x8{s0[8], s0[9], s0[10], s0[11], s0[12], s0[13], s0[14], s0[15]});
-          pk[2] = pack8<F16>(f32x8{s1[0], s1[1], s1[2], s1[3], s1[4], s1[5], s1[6], s1[7]});
-          pk[3] = pack8<F16>(f32x8{s1[8], s1[9], s1[10], s1[11], s1[12], s1[13], s1[14], s1[15]});
-          // O^T += V^T P^T
-          const uint16_t* vl = stage + K_ELEMS + ql * VS + hl * 8;
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-              const u32x4 vop = *(const u32x4*)(vl + dt * 32 * VS + ks * 16);
-              acc[dt] = mfma32<F16>(vop, pk[ks], acc[dt]);
-            }
-          }
-        }
-        buf ^= 1;
-        s = sn;
-      }
-
-      // ---------------------------------------------------------------- epilogue
-      const float l_tot = pair_sum(l_run, partner);
-      const int q = qfirst + wave * 32 + ql;
-      uint16_t* op = a.o + b * a.o_sb + h * a.o_sh + (int64_t)q * a.o_sn + hl * 4;
-      float* lsep = a.lse ? a.lse + (int64_t)bh * a.tokens + q : nullptr;
-      if (!is_global || a.nsplit == 1) {
-        const float inv = 1.f / l_tot;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            u32x2 w = {pack2<F16>(acc[dt][gq * 4 + 0] * inv, acc[dt][gq * 4 + 1] * inv),
-                       pack2<F16>(acc[dt][gq * 4 + 2] * inv, acc[dt][gq * 4 + 3] * inv)};
-            *(u32x2*)(op + dt * 32 + gq * 8) = w;
-          }
-        if (lsep && hl == 0) *lsep = (m_run + __log2f(l_tot)) * LN2;
-      } else {
-        // split global tile: publish the partial, the last chunk merges all of them
-        const int tile = bh * a.global_tiles + gtile;
-        const int64_t slot = (int64_t)tile * a.nsplit + split;
-        constexpr int FRAG = DT * 16 * 64;
-        float* pa = a.part + (slot * WAVES + wave) * FRAG;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) pa[(dt * 16 + i) * 64 + lane] = acc[dt][i];
-        float* pml = a.part_ml + (slot * WAVES + wave) * 128;
-        pml[lane] = m_run;
-        pml[64 + lane] = l_tot;
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) s_last = atomicAdd(&a.counters[16 + tile], 1) == a.nsplit - 1;
-        __syncthreads();
-        if (s_last) {
-          __threadfence();
-          float mmax = -__builtin_inff();
-          for (int c = 0; c < a.nsplit; ++c) {
-            const float* pm = a.part_ml + (((int64_t)tile * a.nsplit + c) * WAVES + wave) * 128;
-            mmax = fmaxf(mmax, __builtin_nontemporal_load(pm + lane));
-          }
-          f32x16 sum[DT];
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) sum[dt] = f32x16{};
-          float lsum = 0.f;
-          for (int c = 0; c < a.nsplit; ++c) {
-            const int64_t sl = ((int64_t)tile * a.nsplit + c) * WAVES + wave;
-            const float* pm = a.part_ml + sl * 128;
-            const float w = fast_exp2(__builtin_nontemporal_load(pm + lane) - mmax);
-            lsum += w * __builtin_nontemporal_load(pm + 64 + lane);
-            const float* pc = a.part + sl * FRAG;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-              for (int i = 0; i < 16; ++i)
-                sum[dt][i] += w * __builtin_nontemporal_load(pc + (dt * 16 + i) * 64 + lane);
-          }
-          const float inv = 1.f / lsum;
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int gq = 0; gq < 4; ++gq) {
-              u32x2 w = {pack2<F16>(sum[dt][gq * 4 + 0] * inv, sum[dt][gq * 4 + 1] * inv),
-                         pack2<F16>(sum[dt][gq * 4 + 2] * inv, sum[dt][gq * 4 + 3] * inv)};
-              *(u32x2*)(op + dt * 32 + gq * 8) = w;
-            }
-          if (lsep && hl == 0) *lsep = (mmax + __log2f(lsum)) * LN2;
-          if (tid == 0) atomicExch(&a.counters[16 + tile], 0);
-        }
-      }
+  // ------------------------------------------------------------------ persistent work queues
+  // Queue x (= blockIdx % nq, the XCD of the round-robin dispatch) owns the contiguous range
+  // [lo(x), hi(x)) of the item list (per (batch, head): global chunks, then ordinary rows), so the
+  // items running on one XCD share heads and neighbouring K/V tiles in its L2.  Workgroups claim
+  // items from their own queue with an atomic counter and steal from the others once it is empty.
+  // The claim for the item after next is issued at an item boundary and consumed one step later,
+  // so its latency hides behind compute; the last workgroup to leave resets the counters.
+  __shared__ int s_claim[2];
+  const int nq = gridDim.x < QUEUES ? (int)gridDim.x : QUEUES;
+  const int qx = blockIdx.x % nq;
+  const int64_t total = (int64_t)a.bh * a.per_bh;
+  auto q_lo = [&](int q) { return (int)(total * q / nq); };
+  auto q_len = [&](int q) { return (int)(total * (q + 1) / nq) - (int)(total * q / nq); };
+  // tid 0 only: global index of a claimed item, or -1 when every queue is drained.
+  auto claim_from = [&](int first_count) {
+    if (first_count < q_len(qx)) return q_lo(qx) + first_count;
+    for (int t = 1; t < nq; ++t) {
+      const int q = (qx + t) % nq;
+      const int c = atomicAdd(&a.counters[q], 1);
+      if (c < q_len(q)) return q_lo(q) + c;
     }
-  }
-  // the last workgroup to leave resets the queue heads for the next launch on this workspace
-  __syncthreads();
+    return -1;
+  };
   if (tid == 0) {
-    __threadfence();
-    if (atomicAdd(&a.counters[QUEUES], 1) == (int)gridDim.x - 1) {
-      for (int i = 0; i <= QUEUES; ++i) atomicExch(&a.counters[i], 0);
+    s_claim[0] = claim_from(atomicAdd(&a.counters[qx], 1));
+    s_claim[1] = claim_from(atomicAdd(&a.counters[qx], 1));
+  }
+  __syncthreads();
+
+  struct Item {
+    int valid, bh, b, h, global, qfirst, row, gtile, split, first_block, nsteps;
+  };
+  auto decode = [&](int idx) {
+    Item it;
+    it.valid = idx >= 0;
+    const int i = it.valid ? idx : 0;
+    it.bh = i / a.per_bh;
+    const int rem = i - it.bh * a.per_bh;
+    it.b = it.bh / a.heads;
+    it.h = it.bh - it.b * a.heads;
+    it.global = rem < a.global_tiles * a.nsplit;
+    it.row = 0;
+    it.gtile = 0;
+    it.split = 0;
+    it.first_block = 0;
+    if (it.global) {
+      it.gtile = rem / a.nsplit;
+      it.split = rem - it.gtile * a.nsplit;
+      it.qfirst = it.gtile * QT;
+      it.first_block = it.split * a.chunk;
+      it.nsteps = min(a.chunk, a.key_blocks - it.first_block);
+    } else {
+      it.row = rem - a.global_tiles * a.nsplit;
+      it.qfirst = a.tokens - (a.rows - it.row) * QT;  // ordinary rows follow the global prefix
+      it.nsteps = 0;  // from the row count, loaded with the item's table entries
+    }
+    return it;
+  };
+  // First 64 table entries (lane i holds entry i) and the entry count of a row item.
+  auto load_meta = [&](const Item& it, int& cnt, int& t_id, int& t_fl) {
+    cnt = 0;
+    t_id = 0;
+    t_fl = 0;
+    if (!it.valid || it.global) return;
+    const int32_t* ids = a.indices + (int64_t)it.row * a.width;
+    const int32_t* fls = a.flags + (int64_t)it.row * a.width;
+    cnt = a.counts[it.row];
+    if (lane < a.width) {
+      t_id = ids[lane];
+      if (HALVES == 2) t_fl = fls[lane];
+    }
+  };
+
+  Item cur = decode(uniform(s_claim[0]));
+  int nxt_idx = uniform(s_claim[1]);  // next item, decoded only when it becomes current
+  int c_cnt, t_id, t_fl, n_cnt, n_id, n_fl;
+  load_meta(cur, c_cnt, t_id, t_fl);
+  load_meta(decode(nxt_idx), n_cnt, n_id, n_fl);
+  if (!cur.global) cur.nsteps = max(uniform(c_cnt), 1) * KBR;
+  int tbase = 0;
+  int pending = 0;       // tid 0: raw counter value of the claim in flight
+  bool claiming = false; // a claim was issued at the last item boundary
+
+  // Block index and per-half permission bits (bit h: query half h may see it) of step s of the
+  // current item.  Table entries live in lane registers; a step reads its entry with v_readlane,
+  // refilling 64 entries at a time for rows longer than 64 entries.
+  auto step_info = [&](int s, int& kb, int& fl) {
+    if (cur.global) {
+      kb = cur.first_block + s;
+      fl = 3;
+      return;
+    }
+    const int e = s / KBR;
+    const int sub = s - e * KBR;
+    if (e >= tbase + 64) {
+      tbase = e & ~63;
+      const int ee = tbase + lane;
+      const bool ok = ee < a.width;
+      t_id = ok ? a.indices[(int64_t)cur.row * a.width + ee] : 0;
+      t_fl = (HALVES == 2 && ok) ? a.flags[(int64_t)cur.row * a.width + ee] : 0;
+      // Wait here, inside the refill branch, for the entries read just below: left pending past
+      // the branch, the waitcnt pass would stall the next LDS reads on every path (vmcnt(0)).
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    }
+    kb = __builtin_amdgcn_readlane(t_id, e - tbase) * KBR + sub;
+    fl = HALVES == 2 ? (__builtin_amdgcn_readlane(t_fl, e - tbase) >> (2 * sub)) & 3 : 1;
+  };
+  auto next_live = [&](int s) {
+    for (; s < cur.nsteps; ++s) {
+      int kb, fl;
+      step_info(s, kb, fl);
+      if (fl) break;
+    }
+    return s;
+  };
+
+  u32x4 qreg[DS];
+  auto load_q = [&](const Item& it) {
+    const uint16_t* qp = a.q + it.b * a.q_sb + it.h * a.q_sh +
+                         (int64_t)(it.qfirst + wave * 32 + ql) * a.q_sn + hl * 8;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) qreg[ds] = *(const u32x4*)(qp + ds * 16);
+  };
+
+  // Stage the K and V tiles of 64-key block kb: wave instruction i covers rows 64*i/CPR.. (64
+  // lanes x 16 bytes = one contiguous KiB of LDS); lane l of it fetches the global chunk that the
+  // swizzle places at LDS slot 64*i + l.  The loads complete asynchronously (vmcnt); the barrier at
+  // the top of the next step waits for them.
+  auto dma_block = [&](uint16_t* stage, int b, int h, int kb) {
+    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh + (int64_t)kb * KEYS * a.k_sn;
+    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh + (int64_t)kb * KEYS * a.v_sn;
+#pragma unroll
+    for (int i0 = 0; i0 < CPR; i0 += WAVES) {
+      const int i = i0 + wave;
+      if (CPR % WAVES == 0 || i < CPR) {
+        const int slot = i * 64 + lane;
+        const int r = slot / CPR;
+        const int c = (slot % CPR) ^ swz<CPR>(r);
+        __builtin_amdgcn_global_load_lds((const void*)(kp + r * a.k_sn + c * 8),
+                                         (lds_ptr)(stage + i * 512), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(vp + r * a.v_sn + c * 8),
+                                         (lds_ptr)(stage + TILE + i * 512), 16, 0, 0);
+      }
+    }
+  };
+
+  // Per-lane LDS element offsets of the MFMA operands (the key-tile and 16-key-step parts are
+  // compile-time offsets added at the read):
+  //  K (A of S^T = K Q^T): row ql, chunk 2*ds + hl, for each d-step ds.
+  //  V (A of O^T = V^T P^T, two transposing reads of 4 keys each): lane (g, j, t) = (lane/16,
+  //  lane%16/4, lane%4) addresses keys 4*hl + j (+8 for the second read) at dims
+  //  32*dt + 16*(g&1) + 4*t; ds_read_b64_tr_b16 then hands lane l the 4 keys at dim 32*dt + ql.
+  int koff[DS];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) koff[ds] = ql * D + (((2 * ds + hl) ^ swz<CPR>(ql)) << 3);
+  int voff[DT][2];
+  {
+    const int g = lane >> 4, j = (lane >> 2) & 3, t = lane & 3;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        const int row = 4 * hl + j + 8 * rb;
+        const int d = 32 * dt + 16 * (g & 1) + 4 * t;
+        voff[dt][rb] = row * D + (((d >> 3) ^ swz<CPR>(row)) << 3) + (d & 7);
+      }
+  }
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
+  float m_run = -__builtin_inff();
+  float l_run = 0.f;
+
+  // Epilogue of the current item: normalised output (and LSE), or, for a chunk of a split global
+  // tile, its partial (unnormalised acc, max, sum) in fragment order; merge_kernel combines the
+  // chunks after this kernel (the kernel boundary makes every partial visible on every XCD).
+  auto epilogue = [&]() {
+    const float l_tot = pair_sum(l_run, partner);
+    const int q = cur.qfirst + wave * 32 + ql;
+    uint16_t* op = a.o + cur.b * a.o_sb + cur.h * a.o_sh + (int64_t)q * a.o_sn + hl * 4;
+    float* lsep = a.lse ? a.lse + (int64_t)cur.bh * a.tokens + q : nullptr;
+    if (!cur.global || a.nsplit == 1) {
+      const float inv = 1.f / l_tot;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          u32x2 w = {pack2<F16>(acc[dt][gq * 4 + 0] * inv, acc[dt][gq * 4 + 1] * inv),
+                     pack2<F16>(acc[dt][gq * 4 + 2] * inv, acc[dt][gq * 4 + 3] * inv)};
+          *(u32x2*)(op + dt * 32 + gq * 8) = w;
+        }
+      if (lsep && hl == 0) *lsep = (m_run + __log2f(l_tot)) * LN2;
+      return;
+    }
+    const int tile = cur.bh * a.global_tiles + cur.gtile;
+    const int64_t slot = (int64_t)tile * a.nsplit + cur.split;
+    float* pa = a.part + (slot * WAVES + wave) * FRAG;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) pa[(dt * 16 + i) * 64 + lane] = acc[dt][i];
+    float* pml = a.part_ml + (slot * WAVES + wave) * 128;
+    pml[lane] = m_run;
+    pml[64 + lane] = l_tot;
+  };
+
+  // ------------------------------------------------------------------ main loop
+  // Every item's step 0 is live (its first key block is global, which both query halves see).
+  // The K/V prefetch runs one step ahead across item boundaries, and the next item's Q is
+  // loaded right after the last score MFMAs of the current item.
+  if (cur.valid) {
+  load_q(cur);
+  {
+    int kb, fl;
+    step_info(0, kb, fl);
+    dma_block(lds0, cur.b, cur.h, kb);
+  }
+  int s = 0;
+  // One step on `stage` while the next block streams into `other`.  The two stages are distinct
+  // LDS arrays and the loop below alternates them at compile time, so the compiler can see that
+  // reads of `stage` never alias the loads in flight into `other`.  Returns true when done.
+  auto step = [&](uint16_t* __restrict__ stage, uint16_t* __restrict__ other) -> bool {
+    int kb, fl;
+    step_info(s, kb, fl);
+    if (claiming && tid == 0) s_claim[0] = claim_from(pending);
+    // every wave's loads of this stage have landed (the barrier's fence waits on vmcnt), and every
+    // wave is done reading the other stage, which the next block's loads may now overwrite
+    __syncthreads();
+    if (claiming) {
+      claiming = false;
+      nxt_idx = uniform(s_claim[0]);
+      load_meta(decode(nxt_idx), n_cnt, n_id, n_fl);
+    }
+    const int sn = next_live(s + 1);
+    const bool cross = sn >= cur.nsteps;
+    if (!cross) {
+      int kbn, fln;
+      step_info(sn, kbn, fln);
+      dma_block(other, cur.b, cur.h, kbn);
+    } else if (nxt_idx >= 0) {
+      const Item nxt = decode(nxt_idx);
+      const int kbn = nxt.global ? nxt.first_block : __builtin_amdgcn_readlane(n_id, 0) * KBR;
+      dma_block(other, nxt.b, nxt.h, kbn);
+    }
+    const bool live = (fl >> half) & 1;
+    const bool q_next = cross && nxt_idx >= 0;
+    {
+      // S^T = K Q^T for two 32-key tiles.  The K operands of two d-steps stay in flight ahead of
+      // the MFMAs (software pipelined LDS reads), so no MFMA waits on a fresh LDS read.
+      f32x16 s0 = f32x16{}, s1 = f32x16{};
+      u32x4 kr[2 * DS];
+#pragma unroll
+      for (int ds = 0; ds < 2; ++ds) {
+        kr[2 * ds] = *(const u32x4*)(stage + koff[ds]);
+        kr[2 * ds + 1] = *(const u32x4*)(stage + koff[ds] + 32 * D);
+      }
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        if (ds + 2 < DS) {
+          kr[2 * ds + 4] = *(const u32x4*)(stage + koff[ds + 2]);
+          kr[2 * ds + 5] = *(const u32x4*)(stage + koff[ds + 2] + 32 * D);
+        }
+        s0 = mfma32<F16>(kr[2 * ds], qreg[ds], s0);
+        s1 = mfma32<F16>(kr[2 * ds + 1], qreg[ds], s1);
+      }
+      // order: 4 K reads, then (2 reads, 2 MFMAs) per d-step, the last two d-steps MFMAs only
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 4, 0);
+#pragma unroll
+      for (int ds = 0; ds < DS - 2; ++ds) {
+        __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4, 0);
+      if (q_next) load_q(decode(nxt_idx));  // the current Q is dead after the score MFMAs
+      // online softmax for query ql (this lane holds 32 of its 64 keys)
+      float mx = s0[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s0[i]);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s1[i]);
+      // A block this wave's query half may not see (paired flags) is computed but masked: its row
+      // max counts as -inf (no rescale) and its exponent offset is -inf, so P = 0 exactly.
+      mx = live ? pair_max(mx, partner) * a.scale_log2 : -__builtin_inff();
+      // Lazy rescale: the exponent reference m_run moves only when some row's max exceeds it by
+      // more than 2^8, so P = exp2(s - m_run) < 256 (exact range for fp32 state and bf16 P) and
+      // the O rescale runs on few blocks.  O = acc / l does not depend on the choice.
+      if (__ballot(mx > m_run + RESCALE_LOG2) != 0) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = fast_exp2(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+        m_run = m_new;
+      }
+      const float neg = live ? -m_run : -__builtin_inff();
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s0[i] = fast_exp2(__builtin_fmaf(s0[i], a.scale_log2, neg));
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s1[i] = fast_exp2(__builtin_fmaf(s1[i], a.scale_log2, neg));
+      u32x4 pk[4];
+      pk[0] = pack8<F16>(f32x8{s0[0], s0[1], s0[2], s0[3], s0[4], s0[5], s0[6], s0[7]});
+      pk[1] = pack8<F16>(f32x8{s0[8], s0[9], s0[10], s0[11], s0[12], s0[13], s0[14], s0[15]});
+      pk[2] = pack8<F16>(f32x8{s1[0], s1[1], s1[2], s1[3], s1[4], s1[5], s1[6], s1[7]});
+      pk[3] = pack8<F16>(f32x8{s1[8], s1[9], s1[10], s1[11], s1[12], s1[13], s1[14], s1[15]});
+      // row sum of the rounded P that enters the PV product (two chains of dot2)
+      float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        l0 = dot2_sum<F16>(pk[ks][0], l0);
+        l1 = dot2_sum<F16>(pk[ks][1], l1);
+        l0 = dot2_sum<F16>(pk[ks][2], l0);
+        l1 = dot2_sum<F16>(pk[ks][3], l1);
+      }
+      l_run += l0 + l1;
+      // O^T += V^T P^T, V operands read two MFMAs ahead
+      const uint16_t* vt = stage + TILE;
+      constexpr int NPV = 4 * DT;
+      u32x4 vr[NPV];
+      auto vread = [&](int j) {  // operand of MFMA j: d-tile j % DT, key step j / DT
+        const int dt = j % DT, ks = j / DT;
+        const u32x2 lo = read_tr(vt + voff[dt][0] + ks * 16 * D);
+        const u32x2 hi = read_tr(vt + voff[dt][1] + ks * 16 * D);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      };
+#pragma unroll
+      for (int j = 0; j < 2; ++j) vr[j] = vread(j);
+#pragma unroll
+      for (int j = 0; j < NPV; ++j) {
+        if (j + 2 < NPV) vr[j + 2] = vread(j + 2);
+        acc[j % DT] = mfma32<F16>(vr[j], pk[j / DT], acc[j % DT]);
+      }
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 4, 1);
+#pragma unroll
+      for (int j = 0; j < NPV - 2; ++j) {
+        __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 1);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 1);
+      }
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 1);
+    }
+    if (!cross) {
+      s = sn;
+      return false;
+    }
+    epilogue();
+    if (nxt_idx < 0) return true;
+    // Wait here, once per item, for the next item's Q (and with it its first K/V block): with
+    // no load pending on qreg at the loop head, the steady-state steps keep their K/V prefetch in
+    // flight across the whole compute of a step.
+    __builtin_amdgcn_s_waitcnt(0);
+    // advance to the next item (table entries loaded one item ahead) and claim the one after it
+    cur = decode(nxt_idx);
+    t_id = n_id;
+    t_fl = n_fl;
+    tbase = 0;
+    if (!cur.global) cur.nsteps = max(uniform(n_cnt), 1) * KBR;
+    if (tid == 0) pending = atomicAdd(&a.counters[qx], 1);
+    claiming = true;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
+    m_run = -__builtin_inff();
+    l_run = 0.f;
+    s = 0;
+    return false;
+  };
+  for (;;) {
+    if (step(lds0, lds1)) break;
+    if (step(lds1, lds0)) break;
+  }
+  }
+  // the last workgroup to leave resets the queue counters for the next launch
+  __syncthreads();
+  if (tid == 0 && atomicAdd(&a.counters[QUEUES], 1) == (int)gridDim.x - 1) {
+    for (int q = 0; q <= QUEUES; ++q) atomicExch(&a.counters[q], 0);
+  }
+}
+
+// Combines the chunks of each split global query tile: O = sum_c 2^(m_c - M) acc_c / L with
+// M = max_c m_c and L = sum_c 2^(m_c - M) l_c; LSE = (M + log2 L) ln 2.  One workgroup per tile,
+// thread (wave, lane) owning the same fragment registers as in attn_fwd_kernel.
+template <int HALVES, int D, bool F16>
+__global__ __launch_bounds__(128 * HALVES) void merge_kernel(AttnArgs a) {
+  constexpr int WAVES = 2 * HALVES;
+  constexpr int QT = 64 * HALVES;
+  constexpr int DT = D / 32;
+  constexpr int FRAG = DT * 16 * 64;
+  const int tile = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ql = lane & 31, hl = lane >> 5;
+  const int bh = tile / a.global_tiles, gtile = tile - bh * a.global_tiles;
+  const int b = bh / a.heads, h = bh - b * a.heads;
+  const int64_t sl0 = (int64_t)tile * a.nsplit * WAVES + wave;
+  float mc[MAX_SPLIT], mmax = -__builtin_inff();
+#pragma unroll
+  for (int c = 0; c < MAX_SPLIT; ++c) {
+    mc[c] = c < a.nsplit ? a.part_ml[(sl0 + c * WAVES) * 128 + lane] : -__builtin_inff();
+    mmax = fmaxf(mmax, mc[c]);
+  }
+  float lsum = 0.f;
+#pragma unroll
+  for (int c = 0; c < MAX_SPLIT; ++c) {
+    if (c < a.nsplit) {
+      mc[c] = fast_exp2(mc[c] - mmax);
+      lsum += mc[c] * a.part_ml[(sl0 + c * WAVES) * 128 + 64 + lane];
     }
   }
+  const float inv = 1.f / lsum;
+  const int q = gtile * QT + wave * 32 + ql;
+  uint16_t* op = a.o + b * a.o_sb + h * a.o_sh + (int64_t)q * a.o_sn + hl * 4;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    f32x16 sum = f32x16{};
+#pragma unroll
+    for (int c = 0; c < MAX_SPLIT; ++c) {
+      if (c < a.nsplit) {
+        const float* pc = a.part + (sl0 + c * WAVES) * FRAG + dt * 16 * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sum[i] += mc[c] * pc[i * 64];
+      }
+    }
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      u32x2 w = {pack2<F16>(sum[gq * 4 + 0] * inv, sum[gq * 4 + 1] * inv),
+                 pack2<F16>(sum[gq * 4 + 2] * inv, sum[gq * 4 + 3] * inv)};
+      *(u32x2*)(op + dt * 32 + gq * 8) = w;
+    }
+  }
+  if (a.lse && hl == 0) a.lse[(int64_t)bh * a.tokens + q] = (mmax + __log2f(lsum)) * LN2;
 }
 
 struct Plan {
@@ -444,18 +619,17 @@ int make_plan(Plan& p, int batch, int heads, int tokens, int head_dim, int globa
   p.rows = (tokens - global_tokens) / p.qt;
   p.key_blocks = tokens / 64;
   p.global_tiles = all_queries ? global_tokens / p.qt : 0;
-  int chunk = width * p.kbr;
-  chunk = chunk < 16 ? 16 : chunk;
-  const int min_chunk = (p.key_blocks + 63) / 64;
-  chunk = chunk < min_chunk ? min_chunk : chunk;
-  p.chunk = chunk;
-  p.nsplit = (p.key_blocks + chunk - 1) / chunk;
+  // A global query tile sweeps every key block; it is split into at most MAX_SPLIT chunks, each
+  // no shorter than the longest ordinary row, so no item dominates the schedule.
+  const int row_steps = width * p.kbr;
+  int nsplit = (p.key_blocks + row_steps - 1) / row_steps;
+  nsplit = nsplit < 1 ? 1 : (nsplit > MAX_SPLIT ? MAX_SPLIT : nsplit);
+  p.chunk = (p.key_blocks + nsplit - 1) / nsplit;
+  p.nsplit = (p.key_blocks + p.chunk - 1) / p.chunk;
   p.per_bh = p.global_tiles * p.nsplit + p.rows;
   const int64_t bh = (int64_t)batch * heads;
   const int64_t tiles = bh * p.global_tiles;
-  HB_REQUIRE(tiles <= MAX_SPLIT_TILES, "too many global query tiles (%lld > %lld)",
-             (long long)tiles, (long long)MAX_SPLIT_TILES);
-  p.counters_bytes = COUNTER_BYTES;
+  p.counters_bytes = 256;
   const int64_t slots = p.nsplit > 1 ? tiles * p.nsplit * p.waves : 0;
   p.part_bytes = slots * (head_dim / 32) * 16 * 64 * 4;
   p.ml_bytes = slots * 128 * 4;
@@ -466,6 +640,9 @@ template <int HALVES, int D, int KBR, bool F16>
 void launch(const AttnArgs& a, int groups, hipStream_t stream) {
   hipLaunchKernelGGL((attn_fwd_kernel<HALVES, D, KBR, F16>), dim3(groups), dim3(128 * HALVES), 0,
                      stream, a);
+  const int tiles = a.bh * a.global_tiles;
+  if (a.nsplit > 1 && tiles > 0)
+    hipLaunchKernelGGL((merge_kernel<HALVES, D, F16>), dim3(tiles), dim3(128 * HALVES), 0, stream, a);
 }
 
 template <int HALVES, int KBR>

@@ -29,8 +29,9 @@ int hb_version(void);
 
 /* ---------------------------------------------------------------- (c) block-sparse attention
  * Workspace needed by hb_paired_fwd / hb_block_sparse_fwd for these shapes (bytes, or -1 when
- * the shapes are rejected).  The workspace must start zero-filled once; the kernels leave their
- * counters at zero when they finish, so one workspace serves every later launch on one stream.
+ * the shapes are rejected).  It holds the work-queue counters (first 256 bytes) and the partial
+ * results of split global query tiles.  It must be zero-filled once before first use; every
+ * launch leaves the counters at zero again, so one workspace serves all later launches.
  * Launches that overlap in time must not share a workspace.
  */
 int64_t hb_attention_workspace_bytes(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
