@@ -64,6 +64,26 @@ def q10(xs, q):
     return xs[min(len(xs) - 1, int(q * len(xs)))]
 
 
+def profiled_traffic(config):
+    """HBM bytes per attention launch from the committed rocprofv3 counter summary, if any.
+
+    FETCH_SIZE and WRITE_SIZE come from two separate `rocprofv3 --pmc` runs of this script,
+    each scaled by what the counter reads for a plain copy of known size; the summary file
+    records the commands, the raw counters and the scaling.  Counters cannot be read from
+    inside this process, so the figure is the profiled one, named with its source.
+    """
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"attn_fwd_{config}_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1]), os.path.relpath(path, os.path.dirname(path) + "/..")
+    except OSError:
+        pass
+    return None, None
+
+
 def live_blocks(meta):
     flags = meta.kv_flags.cpu()
     counts = meta.kv_counts.cpu()
@@ -118,7 +138,7 @@ def main():
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py runs on one GPU: --gpus {a.gpus} is not supported in this build "
-              "(the heads shard with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(the 24 heads would shard across GPUs with no exchange)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -239,6 +259,7 @@ def main():
                 permute=perm,
             )
 
+    traffic, traffic_src = profiled_traffic(a.config)
     result = {
         "metric": "sparse-attn fwd ms + live-block MFMA util, FLUX 2048px 16-tile K3 vs dense",
         "value": round(weighted, 4),
@@ -276,7 +297,8 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
         },
         **extras,
     }

@@ -5,8 +5,7 @@
  * Return value: 0 on success, HB_EINVAL (1) for a rejected argument, HB_EHIP (2) for a HIP
  * runtime error; hb_last_error() gives the message (thread-local).
  *
- * Python binds these through ctypes (hilberta_amd/_lib.py); INTEGRATION.md shows the binding
- * the reference package would add.
+ * Python binds these through ctypes (hilberta_amd/_lib.py).
  */
 #ifndef HILBERTA_HIP_H
 #define HILBERTA_HIP_H
