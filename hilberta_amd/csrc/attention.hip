@@ -5,7 +5,7 @@
 //
 //  * Work item = one query tile (128 queries for paired tables, 64 for unpaired ones) of one
 //    (batch, head), or one chunk of a global (text) query tile's all-key sweep.  Global tiles are
-//    split into at most 4 chunks, none shorter than the longest ordinary row, so no item
+//    split into at most MAX_SPLIT chunks, none shorter than the longest ordinary row, so no item
 //    dominates the schedule; chunk partials (unnormalised accumulator, running max, row sum) go to
 //    the workspace and merge_kernel combines them after the main kernel.
 //  * Persistent workgroups (2 per CU) claim items from 8 work queues, one per XCD (queue x =
@@ -13,19 +13,21 @@
 //    so items that share K/V blocks run under one L2; idle workgroups steal from other queues.
 //    Claims run one item ahead, and the next item's table entries, first K/V block and Q tile are
 //    prefetched while the current item finishes, so no claim or load latency sits between items.
-//  * Per 64-key block: K (row major) and V (transposed, keys permuted to the MFMA operand order)
-//    are staged through double-buffered LDS; the next block's global loads are in flight while the
-//    current block is computed.  Blocks whose flags allow neither query half are never loaded.
+//  * Per 64-key block: the K and V tiles stream from HBM straight into one of two LDS stages
+//    (global_load_lds, 16 bytes per lane, rows unpadded with an XOR chunk swizzle); the next
+//    block's loads are in flight while the current block is computed.  Table entries that neither
+//    query half may see are never loaded.
 //  * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16: each lane then
 //    holds 16 keys of ONE query, so the online-softmax row max is an in-lane max plus one
-//    permlane32 swap, and the output O^T = V^T P^T reuses the score registers directly as the
-//    B operand (no shuffle of P) while the rescale by alpha is a per-lane scalar.
-//  * Each wave owns 32 queries; in paired mode waves 0-1 own query half 0 and waves 2-3 half 1, so
-//    the flag test (flags >> (half + 2*key_half)) & 1 of paired_kernel.py:65,83-84 is a
-//    wave-uniform skip.
-//  * Online softmax in exp2 with fp32 state (paired_kernel.py:82-93); P is rounded to the input
-//    type before the PV product as in the reference; an optional fp32 per-row logsumexp (natural
-//    log) is written as well.
+//    cross-half exchange (ds_bpermute), and the output O^T = V^T P^T takes the score registers
+//    directly as the B operand; its A operand (V^T) comes out of LDS already transposed through
+//    ds_read_b64_tr_b16.
+//  * Each wave owns 32 queries; in paired mode waves 0-1 own query half 0 and waves 2-3 half 1.
+//    A block that the flag test (flags >> (half + 2*key_half)) & 1 of paired_kernel.py:65,83-84
+//    hides from a wave's half is computed but masked (P = 0), which keeps one code path.
+//  * Online softmax in exp2 with fp32 state (paired_kernel.py:82-93) and a lazy rescale; P is
+//    rounded to the input type before the PV product as in the reference; an optional fp32
+//    per-row logsumexp (natural log) is written as well.
 #include "common.h"
 #include "../../include/hilberta_hip.h"
 
@@ -36,7 +38,12 @@ constexpr int KEYS = 64;     // keys per staged block
 constexpr float LN2 = 0.69314718055994530942f;
 constexpr int QUEUES = 8;    // one work queue per XCD
 constexpr float RESCALE_LOG2 = 8.0f;  // lazy-rescale threshold (log2 units)
-constexpr int MAX_SPLIT = 16;         // chunks per global query tile
+constexpr int MAX_SPLIT = 16;  // chunks per global query tile, at most
+#ifndef HB_SPLIT_DIV
+#define HB_SPLIT_DIV 1
+#endif
+constexpr int SPLIT_DIV = HB_SPLIT_DIV;
+constexpr int NOMINAL_GROUPS = 512;  // persistent workgroups on a full MI355X (2 per CU)
 // __builtin_amdgcn_sched_group_barrier instruction classes
 constexpr int SG_MFMA = 0x008;
 constexpr int SG_DS_READ = 0x100;
@@ -166,25 +173,37 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   const int partner = (lane ^ 32) << 2;
 
   // ------------------------------------------------------------------ persistent work queues
-  // Queue x (= blockIdx % nq, the XCD of the round-robin dispatch) owns the contiguous range
-  // [lo(x), hi(x)) of the item list (per (batch, head): global chunks, then ordinary rows), so the
-  // items running on one XCD share heads and neighbouring K/V tiles in its L2.  Workgroups claim
-  // items from their own queue with an atomic counter and steal from the others once it is empty.
-  // The claim for the item after next is issued at an item boundary and consumed one step later,
-  // so its latency hides behind compute; the last workgroup to leave resets the counters.
+  // Item codes: [0, total_g) are the chunks of global query tiles ((batch, head)-major, then tile,
+  // then chunk), [total_g, total_g + total_r) the ordinary rows ((batch, head)-major).  Queue x
+  // (= blockIdx % nq, the XCD of the round-robin dispatch) owns the x-th eighth of each list, so
+  // the items running on one XCD share heads and neighbouring K/V tiles in its L2, and hands out
+  // its global chunks first (longest items first), then its rows.  Workgroups claim items from
+  // their own queue with an atomic counter and steal from the others once it is empty.  The claim
+  // for the item after next is issued at an item boundary and consumed one step later, so its
+  // latency hides behind compute; the last workgroup to leave resets the counters.
   __shared__ int s_claim[2];
   const int nq = gridDim.x < QUEUES ? (int)gridDim.x : QUEUES;
   const int qx = blockIdx.x % nq;
-  const int64_t total = (int64_t)a.bh * a.per_bh;
-  auto q_lo = [&](int q) { return (int)(total * q / nq); };
-  auto q_len = [&](int q) { return (int)(total * (q + 1) / nq) - (int)(total * q / nq); };
-  // tid 0 only: global index of a claimed item, or -1 when every queue is drained.
+  const int gper = a.global_tiles * a.nsplit;  // global chunks per (batch, head)
+  const int total_g = a.bh * gper;
+  const int total_r = a.bh * a.rows;
+  auto g_lo = [&](int q) { return (int)((int64_t)total_g * q / nq); };
+  auto r_lo = [&](int q) { return (int)((int64_t)total_r * q / nq); };
+  // tid 0 only: code of the c-th item of queue q, or -1 past its end
+  auto item_of = [&](int q, int c) {
+    const int gl = g_lo(q + 1) - g_lo(q);
+    if (c < gl) return g_lo(q) + c;
+    c -= gl;
+    return c < r_lo(q + 1) - r_lo(q) ? total_g + r_lo(q) + c : -1;
+  };
+  // tid 0 only: code of a claimed item, or -1 when every queue is drained.
   auto claim_from = [&](int first_count) {
-    if (first_count < q_len(qx)) return q_lo(qx) + first_count;
+    const int own = item_of(qx, first_count);
+    if (own >= 0) return own;
     for (int t = 1; t < nq; ++t) {
       const int q = (qx + t) % nq;
-      const int c = atomicAdd(&a.counters[q], 1);
-      if (c < q_len(q)) return q_lo(q) + c;
+      const int c = item_of(q, atomicAdd(&a.counters[q], 1));
+      if (c >= 0) return c;
     }
     return -1;
   };
@@ -201,26 +220,28 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     Item it;
     it.valid = idx >= 0;
     const int i = it.valid ? idx : 0;
-    it.bh = i / a.per_bh;
-    const int rem = i - it.bh * a.per_bh;
-    it.b = it.bh / a.heads;
-    it.h = it.bh - it.b * a.heads;
-    it.global = rem < a.global_tiles * a.nsplit;
+    it.global = i < total_g;
     it.row = 0;
     it.gtile = 0;
     it.split = 0;
     it.first_block = 0;
     if (it.global) {
+      it.bh = i / gper;
+      const int rem = i - it.bh * gper;
       it.gtile = rem / a.nsplit;
       it.split = rem - it.gtile * a.nsplit;
       it.qfirst = it.gtile * QT;
       it.first_block = it.split * a.chunk;
       it.nsteps = min(a.chunk, a.key_blocks - it.first_block);
     } else {
-      it.row = rem - a.global_tiles * a.nsplit;
+      const int ri = i - total_g;
+      it.bh = ri / a.rows;
+      it.row = ri - it.bh * a.rows;
       it.qfirst = a.tokens - (a.rows - it.row) * QT;  // ordinary rows follow the global prefix
       it.nsteps = 0;  // from the row count, loaded with the item's table entries
     }
+    it.b = it.bh / a.heads;
+    it.h = it.bh - it.b * a.heads;
     return it;
   };
   // First 64 table entries (lane i holds entry i) and the entry count of a row item.
@@ -552,47 +573,46 @@ __global__ __launch_bounds__(128 * HALVES) void merge_kernel(AttnArgs a) {
   constexpr int DT = D / 32;
   constexpr int FRAG = DT * 16 * 64;
   const int tile = blockIdx.x;
+  const int dt = blockIdx.y;  // 32-column slice of the head dimension
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ql = lane & 31, hl = lane >> 5;
   const int bh = tile / a.global_tiles, gtile = tile - bh * a.global_tiles;
   const int b = bh / a.heads, h = bh - b * a.heads;
   const int64_t sl0 = (int64_t)tile * a.nsplit * WAVES + wave;
-  float mc[MAX_SPLIT], mmax = -__builtin_inff();
+  float mc[MAX_SPLIT], lc[MAX_SPLIT], mmax = -__builtin_inff();
 #pragma unroll
   for (int c = 0; c < MAX_SPLIT; ++c) {
-    mc[c] = c < a.nsplit ? a.part_ml[(sl0 + c * WAVES) * 128 + lane] : -__builtin_inff();
-    mmax = fmaxf(mmax, mc[c]);
+    const float* ml = a.part_ml + (sl0 + c * WAVES) * 128 + lane;
+    mc[c] = c < a.nsplit ? ml[0] : -__builtin_inff();
+    lc[c] = c < a.nsplit ? ml[64] : 0.f;
   }
+#pragma unroll
+  for (int c = 0; c < MAX_SPLIT; ++c) mmax = fmaxf(mmax, mc[c]);
   float lsum = 0.f;
 #pragma unroll
   for (int c = 0; c < MAX_SPLIT; ++c) {
-    if (c < a.nsplit) {
-      mc[c] = fast_exp2(mc[c] - mmax);
-      lsum += mc[c] * a.part_ml[(sl0 + c * WAVES) * 128 + 64 + lane];
-    }
+    mc[c] = c < a.nsplit ? fast_exp2(mc[c] - mmax) : 0.f;
+    lsum += mc[c] * lc[c];
   }
   const float inv = 1.f / lsum;
-  const int q = gtile * QT + wave * 32 + ql;
-  uint16_t* op = a.o + b * a.o_sb + h * a.o_sh + (int64_t)q * a.o_sn + hl * 4;
+  f32x16 sum = f32x16{};
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    f32x16 sum = f32x16{};
+  for (int c = 0; c < MAX_SPLIT; ++c) {
+    if (c < a.nsplit) {
+      const float* pc = a.part + (sl0 + c * WAVES) * FRAG + dt * 16 * 64 + lane;
 #pragma unroll
-    for (int c = 0; c < MAX_SPLIT; ++c) {
-      if (c < a.nsplit) {
-        const float* pc = a.part + (sl0 + c * WAVES) * FRAG + dt * 16 * 64 + lane;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sum[i] += mc[c] * pc[i * 64];
-      }
-    }
-#pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      u32x2 w = {pack2<F16>(sum[gq * 4 + 0] * inv, sum[gq * 4 + 1] * inv),
-                 pack2<F16>(sum[gq * 4 + 2] * inv, sum[gq * 4 + 3] * inv)};
-      *(u32x2*)(op + dt * 32 + gq * 8) = w;
+      for (int i = 0; i < 16; ++i) sum[i] += mc[c] * pc[i * 64];
     }
   }
-  if (a.lse && hl == 0) a.lse[(int64_t)bh * a.tokens + q] = (mmax + __log2f(lsum)) * LN2;
+  const int q = gtile * QT + wave * 32 + ql;
+  uint16_t* op = a.o + b * a.o_sb + h * a.o_sh + (int64_t)q * a.o_sn + hl * 4 + dt * 32;
+#pragma unroll
+  for (int gq = 0; gq < 4; ++gq) {
+    u32x2 w = {pack2<F16>(sum[gq * 4 + 0] * inv, sum[gq * 4 + 1] * inv),
+               pack2<F16>(sum[gq * 4 + 2] * inv, sum[gq * 4 + 3] * inv)};
+    *(u32x2*)(op + gq * 8) = w;
+  }
+  if (a.lse && dt == 0 && hl == 0) a.lse[(int64_t)bh * a.tokens + q] = (mmax + __log2f(lsum)) * LN2;
 }
 
 struct Plan {
@@ -619,10 +639,16 @@ int make_plan(Plan& p, int batch, int heads, int tokens, int head_dim, int globa
   p.rows = (tokens - global_tokens) / p.qt;
   p.key_blocks = tokens / 64;
   p.global_tiles = all_queries ? global_tokens / p.qt : 0;
-  // A global query tile sweeps every key block; it is split into at most MAX_SPLIT chunks, each
-  // no shorter than the longest ordinary row, so no item dominates the schedule.
-  const int row_steps = width * p.kbr;
-  int nsplit = (p.key_blocks + row_steps - 1) / row_steps;
+  // A global query tile sweeps every key block.  It is split into at most MAX_SPLIT chunks of
+  // about the average work of one workgroup (at the nominal 2 workgroups x 256 CUs), and never
+  // shorter than the longest ordinary row: the chunks are claimed first, so each finishes well
+  // before the queues drain, while few chunks keep the partials and the merge small.
+  const int64_t row_steps = (int64_t)width * p.kbr;
+  const int64_t all_steps =
+      (int64_t)batch * heads * ((int64_t)p.rows * row_steps + (int64_t)p.global_tiles * p.key_blocks);
+  int64_t target = (all_steps + NOMINAL_GROUPS - 1) / NOMINAL_GROUPS / SPLIT_DIV;
+  if (target < row_steps) target = row_steps;
+  int nsplit = (int)((p.key_blocks + target - 1) / target);
   nsplit = nsplit < 1 ? 1 : (nsplit > MAX_SPLIT ? MAX_SPLIT : nsplit);
   p.chunk = (p.key_blocks + nsplit - 1) / nsplit;
   p.nsplit = (p.key_blocks + p.chunk - 1) / p.chunk;
@@ -642,7 +668,8 @@ void launch(const AttnArgs& a, int groups, hipStream_t stream) {
                      stream, a);
   const int tiles = a.bh * a.global_tiles;
   if (a.nsplit > 1 && tiles > 0)
-    hipLaunchKernelGGL((merge_kernel<HALVES, D, F16>), dim3(tiles), dim3(128 * HALVES), 0, stream, a);
+    hipLaunchKernelGGL((merge_kernel<HALVES, D, F16>), dim3(tiles, D / 32), dim3(128 * HALVES), 0,
+                       stream, a);
 }
 
 template <int HALVES, int KBR>
