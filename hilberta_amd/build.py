@@ -66,6 +66,12 @@ def build(verbose: bool = True) -> Path:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
+    # a kernel whose host-side launch stub was not emitted links fine but cannot be loaded
+    undefined = subprocess.run(["nm", "-D", "--undefined-only", str(tmp)], capture_output=True,
+                               text=True).stdout
+    stubs = [line.split()[-1] for line in undefined.splitlines() if "__device_stub__" in line]
+    if stubs:
+        raise RuntimeError(f"link left {len(stubs)} kernel launch stubs undefined, e.g. {stubs[0]}")
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(sources)} sources")

@@ -14,7 +14,7 @@
 //    Claims run one item ahead, and the next item's table entries, first K/V block and Q tile are
 //    prefetched while the current item finishes, so no claim or load latency sits between items.
 //  * Per 64-key block: the K and V tiles stream from HBM straight into one of two LDS stages
-//    (global_load_lds, 16 bytes per lane, rows unpadded with an XOR chunk swizzle); the next
+//    (buffer loads to LDS, 16 bytes per lane, rows unpadded with an XOR chunk swizzle); the next
 //    block's loads are in flight while the current block is computed.  Table entries that neither
 //    query half may see are never loaded.
 //  * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16: each lane then
@@ -44,6 +44,8 @@ constexpr int MAX_SPLIT = 16;  // chunks per global query tile, at most
 #endif
 constexpr int SPLIT_DIV = HB_SPLIT_DIV;
 constexpr int NOMINAL_GROUPS = 512;  // persistent workgroups on a full MI355X (2 per CU)
+// word 3 of a raw buffer resource (32-bit data format, no swizzle), as for gfx9-family buffers
+constexpr int BUFFER_WORD3 = 0x00020000;
 // __builtin_amdgcn_sched_group_barrier instruction classes
 constexpr int SG_MFMA = 0x008;
 constexpr int SG_DS_READ = 0x100;
@@ -126,6 +128,18 @@ __device__ __forceinline__ float dot2_sum(uint32_t pair, float acc) {
 }
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// 16 bytes per lane from base + voffset + soffset (bytes) into LDS at dst + 16 * lane, as a
+// buffer load to LDS over a raw buffer at base.  The buffer resource type exists only for the
+// device target, so the host pass (which compiles the kernels' launch stubs) sees an empty body.
+__device__ __forceinline__ void buffer_load_lds16(const void* base, uint16_t* dst, int voffset,
+                                                  int soffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, BUFFER_WORD3);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr)dst, 16, voffset, soffset, 0, 0);
+#endif
+}
 
 // Chunk permutation of K/V row r in LDS (16-byte chunks, CPR per row): XOR with a row-dependent
 // value so that the K reads (8 consecutive rows, one 16-byte chunk each) and the transposing V
@@ -312,22 +326,30 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
 
   // Stage the K and V tiles of 64-key block kb: wave instruction i covers rows 64*i/CPR.. (64
   // lanes x 16 bytes = one contiguous KiB of LDS); lane l of it fetches the global chunk that the
-  // swizzle places at LDS slot 64*i + l.  The loads complete asynchronously (vmcnt); the barrier at
-  // the top of the next step waits for them.
-  auto dma_block = [&](uint16_t* stage, int b, int h, int kb) {
-    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh + (int64_t)kb * KEYS * a.k_sn;
-    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh + (int64_t)kb * KEYS * a.v_sn;
+  // swizzle places at LDS slot 64*i + l.  The loads are buffer loads to LDS (MUBUF, counted on
+  // vmcnt only, so the LDS reads that follow keep exact lgkmcnt waits) over a raw buffer of the
+  // (batch, head) K or V rows; the per-lane byte offsets inside a block are fixed, the block
+  // offset goes in soffset.  The loads complete asynchronously; the top of the next step waits.
+  constexpr int NDMA = (CPR + WAVES - 1) / WAVES;
+  int dk[NDMA], dv[NDMA];
 #pragma unroll
-    for (int i0 = 0; i0 < CPR; i0 += WAVES) {
-      const int i = i0 + wave;
+  for (int n = 0; n < NDMA; ++n) {
+    const int slot = (n * WAVES + wave) * 64 + lane;
+    const int r = slot / CPR;
+    const int c = (slot % CPR) ^ swz<CPR>(r);
+    dk[n] = (int)(r * a.k_sn + c * 8) * 2;
+    dv[n] = (int)(r * a.v_sn + c * 8) * 2;
+  }
+  auto dma_block = [&](uint16_t* stage, int b, int h, int kb) {
+    const uint16_t* kbase = a.k + b * a.k_sb + h * a.k_sh;
+    const uint16_t* vbase = a.v + b * a.v_sb + h * a.v_sh;
+    const int sk = kb * KEYS * (int)a.k_sn * 2, sv = kb * KEYS * (int)a.v_sn * 2;
+#pragma unroll
+    for (int n = 0; n < NDMA; ++n) {
+      const int i = n * WAVES + wave;
       if (CPR % WAVES == 0 || i < CPR) {
-        const int slot = i * 64 + lane;
-        const int r = slot / CPR;
-        const int c = (slot % CPR) ^ swz<CPR>(r);
-        __builtin_amdgcn_global_load_lds((const void*)(kp + r * a.k_sn + c * 8),
-                                         (lds_ptr)(stage + i * 512), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(vp + r * a.v_sn + c * 8),
-                                         (lds_ptr)(stage + TILE + i * 512), 16, 0, 0);
+        buffer_load_lds16(kbase, stage + i * 512, dk[n], sk);
+        buffer_load_lds16(vbase, stage + TILE + i * 512, dv[n], sv);
       }
     }
   };
@@ -412,8 +434,10 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     int kb, fl;
     step_info(s, kb, fl);
     if (claiming && tid == 0) s_claim[0] = claim_from(pending);
-    // every wave's loads of this stage have landed (the barrier's fence waits on vmcnt), and every
-    // wave is done reading the other stage, which the next block's loads may now overwrite
+    // every wave's loads of this stage have landed (each wave waits for its own, then the
+    // barrier), and every wave is done reading the other stage, which the next block's loads may
+    // now overwrite
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
     if (claiming) {
       claiming = false;
@@ -705,6 +729,9 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, float*
   for (int i = 0; i < 12; ++i)
     HB_REQUIRE(strides[i] > 0 && strides[i] % 8 == 0,
                "Q/K/V/out outer strides must be positive multiples of 8 elements");
+  // K/V blocks are addressed with 32-bit byte offsets from each (batch, head) base
+  HB_REQUIRE(((int64_t)tokens * (strides[5] > strides[8] ? strides[5] : strides[8])) * 2 < (1ll << 31),
+             "K/V token stride too large: one (batch, head) must span less than 2 GiB");
   const int64_t need = p.counters_bytes + p.part_bytes + p.ml_bytes;
   HB_REQUIRE(workspace && workspace_bytes >= need && ((uintptr_t)workspace & 255) == 0,
              "workspace must be 256-byte aligned and hold %lld bytes", (long long)need);
