@@ -43,7 +43,8 @@ constexpr int MAX_SPLIT = 16;  // chunks per global query tile, at most
 #define HB_SPLIT_DIV 1
 #endif
 constexpr int SPLIT_DIV = HB_SPLIT_DIV;
-constexpr int NOMINAL_GROUPS = 512;  // persistent workgroups on a full MI355X (2 per CU)
+constexpr int NOMINAL_GROUPS = 512;
+ // persistent workgroups on a full MI355X (2 per CU)
 // word 3 of a raw buffer resource (32-bit data format, no swizzle), as for gfx9-family buffers
 constexpr int BUFFER_WORD3 = 0x00020000;
 // __builtin_amdgcn_sched_group_barrier instruction classes
@@ -160,9 +161,11 @@ __device__ __forceinline__ u32x2 read_tr(const uint16_t* p) {
 
 template <int HALVES, int D, int KBR, bool F16>
 __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs a) {
-  constexpr int WAVES = 2 * HALVES;
-  constexpr int NT = 64 * WAVES;
+  constexpr int WAVES = 2 * HALVES;             // waves per workgroup, 32 queries each
   constexpr int QT = 64 * HALVES;               // queries per work item
+  constexpr int NG = 1;                         // 32-query groups per wave
+  constexpr int QW = 32 * NG;                   // queries per wave
+  constexpr int VW = WAVES * NG;                // 32-query groups per item
   constexpr int CPR = D / 8;                    // 16-byte chunks per K/V row
   constexpr int TILE = KEYS * D;                // elements of one K (or V) tile
   constexpr int STAGE = 2 * TILE;               // K tile then V tile
@@ -181,7 +184,7 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   // wave index as a provably uniform (scalar) value, so per-wave tests such as the flag check
   // compile to branches rather than exec-masked code
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = HALVES == 2 ? (wave >> 1) : 0;
+  const int half = HALVES == 2 ? (wave * QW) / 64 : 0;
   const int ql = lane & 31;   // query (column) owned by this lane inside the wave's 32
   const int hl = lane >> 5;   // lane half: selects the 8-element k slice of MFMA operands
   const int partner = (lane ^ 32) << 2;
@@ -316,12 +319,15 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     return s;
   };
 
-  u32x4 qreg[DS];
+  u32x4 qreg[NG][DS];
   auto load_q = [&](const Item& it) {
-    const uint16_t* qp = a.q + it.b * a.q_sb + it.h * a.q_sh +
-                         (int64_t)(it.qfirst + wave * 32 + ql) * a.q_sn + hl * 8;
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) qreg[ds] = *(const u32x4*)(qp + ds * 16);
+    for (int g = 0; g < NG; ++g) {
+      const uint16_t* qp = a.q + it.b * a.q_sb + it.h * a.q_sh +
+                           (int64_t)(it.qfirst + wave * QW + g * 32 + ql) * a.q_sn + hl * 8;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) qreg[g][ds] = *(const u32x4*)(qp + ds * 16);
+    }
   };
 
   // Stage the K and V tiles of 64-key block kb: wave instruction i covers rows 64*i/CPR.. (64
@@ -331,25 +337,37 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   // (batch, head) K or V rows; the per-lane byte offsets inside a block are fixed, the block
   // offset goes in soffset.  The loads complete asynchronously; the top of the next step waits.
   constexpr int NDMA = (CPR + WAVES - 1) / WAVES;
-  int dk[NDMA], dv[NDMA];
+  // When one round of the waves' instructions covers a multiple of 16 rows, the swizzle repeats
+  // and instruction n's lane offsets are instruction 0's plus a uniform row offset, which goes
+  // in soffset: one offset register per tile instead of NDMA.
+  constexpr int ROWS_PER_ROUND = WAVES * 64 / CPR;
+  constexpr bool DMA_LINEAR = ROWS_PER_ROUND % 16 == 0;
+  constexpr int NOFF = DMA_LINEAR ? 1 : NDMA;
+  int dk[NOFF], dv[NOFF];
 #pragma unroll
-  for (int n = 0; n < NDMA; ++n) {
+  for (int n = 0; n < NOFF; ++n) {
     const int slot = (n * WAVES + wave) * 64 + lane;
     const int r = slot / CPR;
     const int c = (slot % CPR) ^ swz<CPR>(r);
     dk[n] = (int)(r * a.k_sn + c * 8) * 2;
     dv[n] = (int)(r * a.v_sn + c * 8) * 2;
   }
-  auto dma_block = [&](uint16_t* stage, int b, int h, int kb) {
-    const uint16_t* kbase = a.k + b * a.k_sb + h * a.k_sh;
-    const uint16_t* vbase = a.v + b * a.v_sb + h * a.v_sh;
-    const int sk = kb * KEYS * (int)a.k_sn * 2, sv = kb * KEYS * (int)a.v_sn * 2;
+  // K and V rows of one (batch, head), computed once per item
+  auto k_base = [&](const Item& it) { return a.k + it.b * a.k_sb + it.h * a.k_sh; };
+  auto v_base = [&](const Item& it) { return a.v + it.b * a.v_sb + it.h * a.v_sh; };
+  const int kblk_bytes = KEYS * (int)a.k_sn * 2, vblk_bytes = KEYS * (int)a.v_sn * 2;
+  const int kround_bytes = ROWS_PER_ROUND * (int)a.k_sn * 2;
+  const int vround_bytes = ROWS_PER_ROUND * (int)a.v_sn * 2;
+  auto dma_block = [&](uint16_t* stage, const uint16_t* kbase, const uint16_t* vbase, int kb) {
+    const int sk = kb * kblk_bytes, sv = kb * vblk_bytes;
 #pragma unroll
     for (int n = 0; n < NDMA; ++n) {
       const int i = n * WAVES + wave;
       if (CPR % WAVES == 0 || i < CPR) {
-        buffer_load_lds16(kbase, stage + i * 512, dk[n], sk);
-        buffer_load_lds16(vbase, stage + TILE + i * 512, dv[n], sv);
+        const int o = DMA_LINEAR ? 0 : n;
+        const int rk = DMA_LINEAR ? n * kround_bytes : 0, rv = DMA_LINEAR ? n * vround_bytes : 0;
+        buffer_load_lds16(kbase, stage + i * 512, dk[o], sk + rk);
+        buffer_load_lds16(vbase, stage + TILE + i * 512, dv[o], sv + rv);
       }
     }
   };
@@ -376,55 +394,65 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
       }
   }
 
-  f32x16 acc[DT];
+  f32x16 acc[NG][DT];
+  float m_run[NG], l_run[NG];
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
-  float m_run = -__builtin_inff();
-  float l_run = 0.f;
+  for (int g = 0; g < NG; ++g) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[g][dt] = f32x16{};
+    m_run[g] = -__builtin_inff();
+    l_run[g] = 0.f;
+  }
 
   // Epilogue of the current item: normalised output (and LSE), or, for a chunk of a split global
   // tile, its partial (unnormalised acc, max, sum) in fragment order; merge_kernel combines the
   // chunks after this kernel (the kernel boundary makes every partial visible on every XCD).
   auto epilogue = [&]() {
-    const float l_tot = pair_sum(l_run, partner);
-    const int q = cur.qfirst + wave * 32 + ql;
-    uint16_t* op = a.o + cur.b * a.o_sb + cur.h * a.o_sh + (int64_t)q * a.o_sn + hl * 4;
-    float* lsep = a.lse ? a.lse + (int64_t)cur.bh * a.tokens + q : nullptr;
-    if (!cur.global || a.nsplit == 1) {
-      const float inv = 1.f / l_tot;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const float l_tot = pair_sum(l_run[g], partner);
+      const int q = cur.qfirst + wave * QW + g * 32 + ql;
+      uint16_t* op = a.o + cur.b * a.o_sb + cur.h * a.o_sh + (int64_t)q * a.o_sn + hl * 4;
+      float* lsep = a.lse ? a.lse + (int64_t)cur.bh * a.tokens + q : nullptr;
+      if (!cur.global || a.nsplit == 1) {
+        const float inv = 1.f / l_tot;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            u32x2 w = {pack2<F16>(acc[g][dt][gq * 4 + 0] * inv, acc[g][dt][gq * 4 + 1] * inv),
+                       pack2<F16>(acc[g][dt][gq * 4 + 2] * inv, acc[g][dt][gq * 4 + 3] * inv)};
+            *(u32x2*)(op + dt * 32 + gq * 8) = w;
+          }
+        if (lsep && hl == 0) *lsep = (m_run[g] + __log2f(l_tot)) * LN2;
+        continue;
+      }
+      // partial slots: (tile, chunk)-major, then the item's 32-query group wave * NG + g
+      const int tile = cur.bh * a.global_tiles + cur.gtile;
+      const int64_t slot = ((int64_t)tile * a.nsplit + cur.split) * VW + wave * NG + g;
+      float* pa = a.part + slot * FRAG;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          u32x2 w = {pack2<F16>(acc[dt][gq * 4 + 0] * inv, acc[dt][gq * 4 + 1] * inv),
-                     pack2<F16>(acc[dt][gq * 4 + 2] * inv, acc[dt][gq * 4 + 3] * inv)};
-          *(u32x2*)(op + dt * 32 + gq * 8) = w;
-        }
-      if (lsep && hl == 0) *lsep = (m_run + __log2f(l_tot)) * LN2;
-      return;
+        for (int i = 0; i < 16; ++i) pa[(dt * 16 + i) * 64 + lane] = acc[g][dt][i];
+      float* pml = a.part_ml + slot * 128;
+      pml[lane] = m_run[g];
+      pml[64 + lane] = l_tot;
     }
-    const int tile = cur.bh * a.global_tiles + cur.gtile;
-    const int64_t slot = (int64_t)tile * a.nsplit + cur.split;
-    float* pa = a.part + (slot * WAVES + wave) * FRAG;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) pa[(dt * 16 + i) * 64 + lane] = acc[dt][i];
-    float* pml = a.part_ml + (slot * WAVES + wave) * 128;
-    pml[lane] = m_run;
-    pml[64 + lane] = l_tot;
   };
 
   // ------------------------------------------------------------------ main loop
   // Every item's step 0 is live (its first key block is global, which both query halves see).
   // The K/V prefetch runs one step ahead across item boundaries, and the next item's Q is
   // loaded right after the last score MFMAs of the current item.
+  const uint16_t* cur_k = k_base(cur);
+  const uint16_t* cur_v = v_base(cur);
   if (cur.valid) {
   load_q(cur);
   {
     int kb, fl;
     step_info(0, kb, fl);
-    dma_block(lds0, cur.b, cur.h, kb);
+    dma_block(lds0, cur_k, cur_v, kb);
   }
   int s = 0;
   // One step on `stage` while the next block streams into `other`.  The two stages are distinct
@@ -449,18 +477,21 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     if (!cross) {
       int kbn, fln;
       step_info(sn, kbn, fln);
-      dma_block(other, cur.b, cur.h, kbn);
+      dma_block(other, cur_k, cur_v, kbn);
     } else if (nxt_idx >= 0) {
       const Item nxt = decode(nxt_idx);
       const int kbn = nxt.global ? nxt.first_block : __builtin_amdgcn_readlane(n_id, 0) * KBR;
-      dma_block(other, nxt.b, nxt.h, kbn);
+      dma_block(other, k_base(nxt), v_base(nxt), kbn);
     }
     const bool live = (fl >> half) & 1;
     const bool q_next = cross && nxt_idx >= 0;
     {
-      // S^T = K Q^T for two 32-key tiles.  The K operands of two d-steps stay in flight ahead of
-      // the MFMAs (software pipelined LDS reads), so no MFMA waits on a fresh LDS read.
-      f32x16 s0 = f32x16{}, s1 = f32x16{};
+      // S^T = K Q^T for two 32-key tiles and each 32-query group.  Every K operand read from LDS
+      // feeds NG MFMAs; the K operands of two d-steps stay in flight ahead of the MFMAs (software
+      // pipelined LDS reads), so no MFMA waits on a fresh LDS read.
+      f32x16 sc[NG][2];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) sc[g][0] = sc[g][1] = f32x16{};
       u32x4 kr[2 * DS];
 #pragma unroll
       for (int ds = 0; ds < 2; ++ds) {
@@ -473,59 +504,77 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
           kr[2 * ds + 4] = *(const u32x4*)(stage + koff[ds + 2]);
           kr[2 * ds + 5] = *(const u32x4*)(stage + koff[ds + 2] + 32 * D);
         }
-        s0 = mfma32<F16>(kr[2 * ds], qreg[ds], s0);
-        s1 = mfma32<F16>(kr[2 * ds + 1], qreg[ds], s1);
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          sc[g][0] = mfma32<F16>(kr[2 * ds], qreg[g][ds], sc[g][0]);
+          sc[g][1] = mfma32<F16>(kr[2 * ds + 1], qreg[g][ds], sc[g][1]);
+        }
       }
-      // order: 4 K reads, then (2 reads, 2 MFMAs) per d-step, the last two d-steps MFMAs only
+      // order: 4 K reads, then (2 reads, 2*NG MFMAs) per d-step, the last two d-steps MFMAs only
       __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 4, 0);
 #pragma unroll
       for (int ds = 0; ds < DS - 2; ++ds) {
         __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2 * NG, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4 * NG, 0);
       if (q_next) load_q(decode(nxt_idx));  // the current Q is dead after the score MFMAs
-      // online softmax for query ql (this lane holds 32 of its 64 keys)
-      float mx = s0[0];
+      // online softmax for query ql of each group (this lane holds 32 of its 64 keys)
+      float mx[NG];
+      bool resc = false;
 #pragma unroll
-      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s0[i]);
+      for (int g = 0; g < NG; ++g) {
+        float m = sc[g][0][0];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s1[i]);
-      // A block this wave's query half may not see (paired flags) is computed but masked: its row
-      // max counts as -inf (no rescale) and its exponent offset is -inf, so P = 0 exactly.
-      mx = live ? pair_max(mx, partner) * a.scale_log2 : -__builtin_inff();
+        for (int i = 1; i < 16; ++i) m = fmaxf(m, sc[g][0][i]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) m = fmaxf(m, sc[g][1][i]);
+        // A block this wave's query half may not see (paired flags) is computed but masked: its
+        // row max counts as -inf (no rescale) and its exponent offset is -inf, so P = 0 exactly.
+        mx[g] = live ? pair_max(m, partner) * a.scale_log2 : -__builtin_inff();
+        resc |= mx[g] > m_run[g] + RESCALE_LOG2;
+      }
       // Lazy rescale: the exponent reference m_run moves only when some row's max exceeds it by
       // more than 2^8, so P = exp2(s - m_run) < 256 (exact range for fp32 state and bf16 P) and
       // the O rescale runs on few blocks.  O = acc / l does not depend on the choice.
-      if (__ballot(mx > m_run + RESCALE_LOG2) != 0) {
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = fast_exp2(m_run - m_new);
-        l_run *= alpha;
+      if (__ballot(resc) != 0) {
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
-        m_run = m_new;
+        for (int g = 0; g < NG; ++g) {
+          const float m_new = fmaxf(m_run[g], mx[g]);
+          const float alpha = fast_exp2(m_run[g] - m_new);
+          l_run[g] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) acc[g][dt] *= alpha;
+          m_run[g] = m_new;
+        }
       }
-      const float neg = live ? -m_run : -__builtin_inff();
+      u32x4 pk[NG][4];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s0[i] = fast_exp2(__builtin_fmaf(s0[i], a.scale_log2, neg));
+      for (int g = 0; g < NG; ++g) {
+        const float neg = live ? -m_run[g] : -__builtin_inff();
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s1[i] = fast_exp2(__builtin_fmaf(s1[i], a.scale_log2, neg));
-      u32x4 pk[4];
-      pk[0] = pack8<F16>(f32x8{s0[0], s0[1], s0[2], s0[3], s0[4], s0[5], s0[6], s0[7]});
-      pk[1] = pack8<F16>(f32x8{s0[8], s0[9], s0[10], s0[11], s0[12], s0[13], s0[14], s0[15]});
-      pk[2] = pack8<F16>(f32x8{s1[0], s1[1], s1[2], s1[3], s1[4], s1[5], s1[6], s1[7]});
-      pk[3] = pack8<F16>(f32x8{s1[8], s1[9], s1[10], s1[11], s1[12], s1[13], s1[14], s1[15]});
-      // row sum of the rounded P that enters the PV product (two chains of dot2)
-      float l0 = 0.f, l1 = 0.f;
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        l0 = dot2_sum<F16>(pk[ks][0], l0);
-        l1 = dot2_sum<F16>(pk[ks][1], l1);
-        l0 = dot2_sum<F16>(pk[ks][2], l0);
-        l1 = dot2_sum<F16>(pk[ks][3], l1);
+          for (int i = 0; i < 16; ++i) sc[g][t][i] = fast_exp2(__builtin_fmaf(sc[g][t][i], a.scale_log2, neg));
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          pk[g][2 * t] = pack8<F16>(f32x8{sc[g][t][0], sc[g][t][1], sc[g][t][2], sc[g][t][3],
+                                          sc[g][t][4], sc[g][t][5], sc[g][t][6], sc[g][t][7]});
+          pk[g][2 * t + 1] = pack8<F16>(f32x8{sc[g][t][8], sc[g][t][9], sc[g][t][10], sc[g][t][11],
+                                              sc[g][t][12], sc[g][t][13], sc[g][t][14], sc[g][t][15]});
+        }
+        // row sum of the rounded P that enters the PV product (two chains of dot2)
+        float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          l0 = dot2_sum<F16>(pk[g][ks][0], l0);
+          l1 = dot2_sum<F16>(pk[g][ks][1], l1);
+          l0 = dot2_sum<F16>(pk[g][ks][2], l0);
+          l1 = dot2_sum<F16>(pk[g][ks][3], l1);
+        }
+        l_run[g] += l0 + l1;
       }
-      l_run += l0 + l1;
-      // O^T += V^T P^T, V operands read two MFMAs ahead
+      // O^T += V^T P^T, V operands read two MFMAs ahead, each feeding NG MFMAs
       const uint16_t* vt = stage + TILE;
       constexpr int NPV = 4 * DT;
       u32x4 vr[NPV];
@@ -540,15 +589,16 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
 #pragma unroll
       for (int j = 0; j < NPV; ++j) {
         if (j + 2 < NPV) vr[j + 2] = vread(j + 2);
-        acc[j % DT] = mfma32<F16>(vr[j], pk[j / DT], acc[j % DT]);
+#pragma unroll
+        for (int g = 0; g < NG; ++g) acc[g][j % DT] = mfma32<F16>(vr[j], pk[g][j / DT], acc[g][j % DT]);
       }
       __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 4, 1);
 #pragma unroll
       for (int j = 0; j < NPV - 2; ++j) {
         __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 1);
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, NG, 1);
       }
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2 * NG, 1);
     }
     if (!cross) {
       s = sn;
@@ -562,6 +612,8 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     __builtin_amdgcn_s_waitcnt(0);
     // advance to the next item (table entries loaded one item ahead) and claim the one after it
     cur = decode(nxt_idx);
+    cur_k = k_base(cur);
+    cur_v = v_base(cur);
     t_id = n_id;
     t_fl = n_fl;
     tbase = 0;
@@ -569,9 +621,12 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     if (tid == 0) pending = atomicAdd(&a.counters[qx], 1);
     claiming = true;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
-    m_run = -__builtin_inff();
-    l_run = 0.f;
+    for (int g = 0; g < NG; ++g) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[g][dt] = f32x16{};
+      m_run[g] = -__builtin_inff();
+      l_run[g] = 0.f;
+    }
     s = 0;
     return false;
   };
