@@ -1,0 +1,151 @@
+"""GPU edge cases of the attention path: table padding, the C ABI's all_queries=0 mode, 4096 px,
+B=2 with BNHD views and 128-key tables at 2048 px, and the permutation at 4096 px sizes.
+
+References are the fp32 oracle formulations in oracle/attention.py (block form on sampled query
+tiles, computed on the device in fp32), the kernel's own all_queries=1 output (bitwise), and
+torch's index_select (bitwise).
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as A
+from tests.helpers import compare, device_paired, oracle_paired, oracle_plan, say
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+
+
+def _sampled_rows_check(out, lse, qd, kd, vd, plan, phase, rows, what, key_block_size=64):
+    """Ordinary paired rows `rows` (64-query blocks) against the block formulation in fp32."""
+    G = plan["global_tokens"]
+    p = plan["phases"][phase]
+    qf, kf, vf = qd.float(), kd.float(), vd.float()
+    for row in rows:
+        q0 = G + 64 * row
+        ids = p["kv_indices"][row, : p["kv_counts"][row]]
+        cols = torch.from_numpy((ids[:, None] * 64 + np.arange(64)).reshape(-1)).to(qd.device)
+        s = torch.matmul(qf[:, :, q0 : q0 + 64], kf[:, :, cols].transpose(-1, -2).contiguous())
+        s = s * D**-0.5
+        rl = torch.logsumexp(s, -1)
+        ro = torch.matmul(torch.softmax(s, -1), vf[:, :, cols])
+        compare(out[:, :, q0 : q0 + 64], None if lse is None else lse[:, :, q0 : q0 + 64], ro, rl,
+                f"{what} row {row}")
+
+
+def test_table_padding_is_ignored(hip_device):
+    """Entries past a row's count may hold anything (sparse_kernel.py:140-152): same bits."""
+    from hilberta_amd.paired_kernel import paired_attention
+
+    plan = oracle_plan("1024_t16k3")
+    q, k, v = (x.to(hip_device) for x in A.seeded_qkv(1, 4, plan["total_tokens"], D, seed=3))
+    meta_np = oracle_paired(plan, 2)
+    clean = device_paired(meta_np, hip_device)
+    ids = meta_np["kv_indices"].copy()
+    flags = meta_np["kv_flags"].copy()
+    counts = meta_np["kv_counts"]
+    width = ids.shape[1]
+    rng = np.random.default_rng(1)
+    pad = np.arange(width)[None, :] >= counts[:, None]
+    assert pad.any(), "the phase needs ragged rows for this test"
+    ids[pad] = rng.integers(-(1 << 30), 1 << 30, size=int(pad.sum()))
+    flags[pad] = rng.integers(0, 16, size=int(pad.sum()))
+    dirty = device_paired(dict(meta_np, kv_indices=ids, kv_flags=flags), hip_device)
+    say("case padding garbage 1024_t16k3 phase 2")
+    a = paired_attention(q, k, v, clean)
+    b = paired_attention(q, k, v, dirty)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_c_abi_all_queries_zero_keeps_global_rows(hip_device):
+    """hb_paired_fwd(all_queries=0) computes only the ordinary rows (the reference's ALL_QUERIES=0
+    launch under global_strategy="flash", paired_kernel.py:173-178) and leaves the global rows."""
+    from hilberta_amd import _lib
+    from hilberta_amd._workspace import attention_workspace
+    from hilberta_amd.paired_kernel import paired_attention
+    from hilberta_amd.sparse_kernel import LOG2E, _strides
+
+    plan = oracle_plan("1024_t4k1")
+    N, G = plan["total_tokens"], plan["global_tokens"]
+    q, k, v = (x.to(hip_device) for x in A.seeded_qkv(1, 6, N, D, seed=4))
+    meta = device_paired(oracle_paired(plan, 1), hip_device)
+    full = paired_attention(q, k, v, meta)
+    out = torch.full_like(q, 7.0)
+    lib = _lib.load()
+    width = meta.kv_indices.shape[1]
+    ws = attention_workspace(q.device, 1, 6, N, D, G, width, 64, paired=1, all_queries=0)
+    strides = (ctypes.c_int64 * 12)(*_strides(q, k, v, out))
+    say("case all_queries=0 via the C ABI")
+    rc = lib.hb_paired_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), None, strides,
+                           1, 6, N, D, 0, meta.kv_indices.data_ptr(), meta.kv_flags.data_ptr(),
+                           meta.kv_counts.data_ptr(), width, G, 64, 0, D**-0.5 * LOG2E,
+                           ws.data_ptr(), ws.numel(), 0, _lib.stream_ptr(q.device))
+    _lib.check(rc, "hb_paired_fwd")
+    torch.cuda.synchronize()
+    assert bool((out[:, :, :G] == 7.0).all()), "global rows were written"
+    assert torch.equal(out[:, :, G:], full[:, :, G:])
+
+
+def test_paired_4096_sampled_rows(hip_device):
+    """4096 px 16-tile K3 (the largest config): global rows on 2 heads and 12 sampled rows."""
+    from hilberta_amd.paired_kernel import paired_attention
+
+    plan = oracle_plan("4096_t16k3")
+    N, G = plan["total_tokens"], plan["global_tokens"]
+    heads = 8
+    q, k, v = (x.to(hip_device) for x in A.seeded_qkv(1, heads, N, D, seed=6))
+    phase = 1
+    meta = device_paired(oracle_paired(plan, phase), hip_device)
+    lse = torch.empty(1, heads, N, dtype=torch.float32, device=hip_device)
+    say("case paired 4096_t16k3 phase 1")
+    out = paired_attention(q, k, v, meta, lse=lse)
+    torch.cuda.synchronize()
+    qf, kf, vf = q[:, :2].float(), k[:, :2].float(), v[:, :2].float()
+    s = torch.matmul(qf[:, :, :G], kf.transpose(-1, -2).contiguous()) * D**-0.5
+    compare(out[:, :2, :G], lse[:, :2, :G], torch.matmul(torch.softmax(s, -1), vf),
+            torch.logsumexp(s, -1), "4096 global rows")
+    del s
+    nq = len(plan["phases"][phase]["kv_counts"])
+    rows = sorted(set(np.random.default_rng(2).choice(nq, 12, replace=False).tolist()) | {0, nq - 1})
+    _sampled_rows_check(out, lse, q, k, v, plan, phase, rows, "4096")
+
+
+def test_paired_2048_batch2_bnhd_key_block_128(hip_device):
+    """B=2, the adapter's BNHD storage viewed as BHND, 128-key paired tables, at 2048 px."""
+    from hilberta_amd.paired_kernel import paired_attention
+
+    plan = oracle_plan("2048_t16k3")
+    N = plan["total_tokens"]
+    heads = 6
+    q, k, v = A.seeded_qkv(2, heads, N, D, seed=8)
+    to_bnhd = lambda x: x.transpose(1, 2).contiguous().to(hip_device).transpose(1, 2)  # noqa: E731
+    qd, kd, vd = to_bnhd(q), to_bnhd(k), to_bnhd(v)
+    meta = device_paired(oracle_paired(plan, 3, key_block_size=128), hip_device)
+    lse = torch.empty(2, heads, N, dtype=torch.float32, device=hip_device)
+    say("case paired 2048 B=2 BNHD KB128 phase 3")
+    out = paired_attention(qd, kd, vd, meta, lse=lse)
+    torch.cuda.synchronize()
+    nq = len(plan["phases"][3]["kv_counts"])
+    rows = sorted(set(np.random.default_rng(3).choice(nq, 16, replace=False).tolist()) | {0, nq - 1})
+    _sampled_rows_check(out, lse, qd, kd, vd, plan, 3, rows, "2048 B=2 KB128")
+
+
+@pytest.mark.parametrize("shape,dim", [((1, 65536, 64), 1), ((1, 66048, 24, 128), 1)])
+def test_permutation_4096_sizes(hip_device, shape, dim):
+    """4096 px latents and BNHD projections: gather and its inverse are bit-exact."""
+    from hilberta_amd.layout import index_select_rows
+
+    gen = torch.Generator("cpu").manual_seed(12)
+    x = torch.randn(shape, generator=gen).to(torch.bfloat16).to(hip_device)
+    index = torch.randperm(shape[dim], generator=gen).to(hip_device)
+    say(f"case permutation {shape}")
+    out = index_select_rows(x, dim, index)
+    assert torch.equal(out, x.index_select(dim, index))
+    inv = torch.empty_like(index)
+    inv[index] = torch.arange(len(index), device=hip_device)
+    assert torch.equal(index_select_rows(out, dim, inv), x)
