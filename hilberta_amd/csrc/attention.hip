@@ -57,7 +57,8 @@ struct AttnArgs {
   const uint16_t* v;
   uint16_t* o;
   float* lse;
-  int64_t q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sn;
+  // element strides (b, h, n) of Q, K, V, O; 32-bit (checked on the host) to save scalar registers
+  int32_t q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sn;
   const int32_t* indices;
   const int32_t* flags;
   const int32_t* counts;
@@ -323,7 +324,7 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   auto load_q = [&](const Item& it) {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      const uint16_t* qp = a.q + it.b * a.q_sb + it.h * a.q_sh +
+      const uint16_t* qp = a.q + (int64_t)it.b * a.q_sb + (int64_t)it.h * a.q_sh +
                            (int64_t)(it.qfirst + wave * QW + g * 32 + ql) * a.q_sn + hl * 8;
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) qreg[g][ds] = *(const u32x4*)(qp + ds * 16);
@@ -353,8 +354,8 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     dv[n] = (int)(r * a.v_sn + c * 8) * 2;
   }
   // K and V rows of one (batch, head), computed once per item
-  auto k_base = [&](const Item& it) { return a.k + it.b * a.k_sb + it.h * a.k_sh; };
-  auto v_base = [&](const Item& it) { return a.v + it.b * a.v_sb + it.h * a.v_sh; };
+  auto k_base = [&](const Item& it) { return a.k + (int64_t)it.b * a.k_sb + (int64_t)it.h * a.k_sh; };
+  auto v_base = [&](const Item& it) { return a.v + (int64_t)it.b * a.v_sb + (int64_t)it.h * a.v_sh; };
   const int kblk_bytes = KEYS * (int)a.k_sn * 2, vblk_bytes = KEYS * (int)a.v_sn * 2;
   const int kround_bytes = ROWS_PER_ROUND * (int)a.k_sn * 2;
   const int vround_bytes = ROWS_PER_ROUND * (int)a.v_sn * 2;
@@ -412,7 +413,7 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     for (int g = 0; g < NG; ++g) {
       const float l_tot = pair_sum(l_run[g], partner);
       const int q = cur.qfirst + wave * QW + g * 32 + ql;
-      uint16_t* op = a.o + cur.b * a.o_sb + cur.h * a.o_sh + (int64_t)q * a.o_sn + hl * 4;
+      uint16_t* op = a.o + (int64_t)cur.b * a.o_sb + (int64_t)cur.h * a.o_sh + (int64_t)q * a.o_sn + hl * 4;
       float* lsep = a.lse ? a.lse + (int64_t)cur.bh * a.tokens + q : nullptr;
       if (!cur.global || a.nsplit == 1) {
         const float inv = 1.f / l_tot;
@@ -684,7 +685,7 @@ __global__ __launch_bounds__(128 * HALVES) void merge_kernel(AttnArgs a) {
     }
   }
   const int q = gtile * QT + wave * 32 + ql;
-  uint16_t* op = a.o + b * a.o_sb + h * a.o_sh + (int64_t)q * a.o_sn + hl * 4 + dt * 32;
+  uint16_t* op = a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)q * a.o_sn + hl * 4 + dt * 32;
 #pragma unroll
   for (int gq = 0; gq < 4; ++gq) {
     u32x2 w = {pack2<F16>(sum[gq * 4 + 0] * inv, sum[gq * 4 + 1] * inv),
@@ -782,8 +783,8 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, float*
   for (int i = 0; i < 4; ++i)
     HB_REQUIRE(((uintptr_t)ptrs[i] & 15) == 0, "Q/K/V/out base pointers must be 16-byte aligned");
   for (int i = 0; i < 12; ++i)
-    HB_REQUIRE(strides[i] > 0 && strides[i] % 8 == 0,
-               "Q/K/V/out outer strides must be positive multiples of 8 elements");
+    HB_REQUIRE(strides[i] > 0 && strides[i] % 8 == 0 && strides[i] < (1ll << 31),
+               "Q/K/V/out outer strides must be positive multiples of 8 elements below 2^31");
   // K/V blocks are addressed with 32-bit byte offsets from each (batch, head) base
   HB_REQUIRE(((int64_t)tokens * (strides[5] > strides[8] ? strides[5] : strides[8])) * 2 < (1ll << 31),
              "K/V token stride too large: one (batch, head) must span less than 2 GiB");
