@@ -15,6 +15,14 @@ phase p measured with HIP events on the launch stream.  Live-block TFLOP/s count
 Also reported: torch SDPA dense attention and this kernel on all-connection tables at the same
 shape, the device table-builder time, permutation bandwidth, and the CPU baseline (fp32 dense
 masked attention of the oracle on the host cores, a bounded sample of heads of the same call).
+
+    python bench.py --denoiser 2048 [--steps K] [--warmup W]
+
+instead times one denoiser step (one whole transformer forward) of a random-init
+FLUX.1-dev-shaped transformer (hilberta_amd/flux_model.py: 19 double + 38 single blocks, hidden
+3072, 24 heads, MLP ratio 4, 512 text tokens, bf16) at 1024 or 2048 px, B=1: dense attention in
+raster order (torch SDPA, the "full" rows) against the persistent Hilbert layout with the paired
+HIP kernel on 4-tile K1 and 16-tile K3 plans, and prints one JSON line for that comparison.
 """
 
 from __future__ import annotations
@@ -123,6 +131,80 @@ def cpu_baseline(q, k, v, meta_phase0, budget_s):
     )
 
 
+# H100 denoiser-forward medians of the reference (real FLUX.1-dev weights), results csv rows
+# 149 / 200 / 188 (1024) and 162 / 204 / 192 (2048): full attention, 4-tile K1, 16-tile K3.
+REFERENCE_DENOISER_MS = {1024: (208.473, 179.918, 177.075), 2048: (1150.413, 712.444, 639.542)}
+
+
+def denoiser_bench(a):
+    """One FLUX-shaped denoiser forward, full attention vs the paired HIP kernel (see --denoiser)."""
+    from hilberta_amd.bridge_k import paired_plan_device
+    from hilberta_amd.flux_model import (FluxShape, FluxTransformer, NativeAttention,
+                                         PersistentAttention, synthetic_inputs)
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    grid = a.denoiser // 16
+    shape = FluxShape()
+    log(f"denoiser {a.denoiser}px: building the random-init model ...")
+    model = FluxTransformer(dev, shape, seed=0)
+    args = synthetic_inputs(dev, grid=grid, batch=a.batch, shape=shape, seed=2707)
+    modes = {"full": NativeAttention()}
+    for tiles, k in ((4, 1), (16, 3)):
+        plan = paired_plan_device(tiles, k, grid_size=grid, device=dev)
+        modes[f"t{tiles}k{k}"] = PersistentAttention(plan, dev, "paired",
+                                                     dict(global_strategy="triton", num_warps=8))
+    steps = max(1, min(a.steps, 10))
+    warmup = max(1, min(a.warmup, 3))
+    ms, outputs = {}, {}
+    t_start = time.perf_counter()
+    for name, attn in modes.items():
+        for _ in range(warmup):
+            outputs[name] = model(**args, attention=attn)
+        torch.cuda.synchronize()
+        times = event_time(lambda attn=attn: model(**args, attention=attn), steps, stream)
+        ms[name] = statistics.median(times)
+        log(f"  {name}: {ms[name]:.2f} ms (median of {steps})")
+    wall_ms = (time.perf_counter() - t_start) * 1e3
+    finite = all(bool(torch.isfinite(o).all()) for o in outputs.values())
+    ref = outputs["full"].float()
+    rel = {name: round(float((o.float() - ref).norm() / ref.norm()), 4)
+           for name, o in outputs.items() if name != "full"}
+    n_img = grid * grid
+    result = {
+        "metric": f"FLUX-shaped denoiser step ms at {a.denoiser}px, paired HIP sparse attn (16-tile K3) "
+        "vs full attn",
+        "value": round(ms["t16k3"], 2),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms["t16k3"], 2),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init weights (seed 0), ~N(0,1) latents / text states (seed 2707)",
+        "config": {
+            "workload": f"FLUX.1-dev-shaped transformer forward at {a.denoiser}px, B={a.batch}, "
+            f"{shape.num_layers}+{shape.num_single_layers} blocks, hidden {shape.hidden}, "
+            f"{shape.heads} heads, 512 text + {n_img} image tokens",
+            "global_batch": a.batch,
+            "seq_len": 512 + n_img,
+            "parallelism": "single GPU",
+        },
+        "denoiser_ms": {name: round(t, 2) for name, t in ms.items()},
+        "speedup_vs_full": {name: round(ms["full"] / t, 3) for name, t in ms.items() if name != "full"},
+        "reference_h100_ms": dict(zip(("full", "t4k1", "t16k3"), REFERENCE_DENOISER_MS[a.denoiser])),
+        "relative_l2_vs_full": rel,
+        "finite": finite,
+        "parameters": model.parameter_count(),
+        "timed_wall_ms": round(wall_ms, 1),
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -133,6 +215,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="attention only (for counter runs)")
+    ap.add_argument("--denoiser", type=int, choices=(1024, 2048), default=0, metavar="PX",
+                    help="time one FLUX-shaped denoiser step at PX (1024 or 2048) instead")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 5 times (calibrates FETCH/WRITE_SIZE)")
     a = ap.parse_args()
@@ -151,6 +235,10 @@ def main():
             y.copy_(x)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": x.numel(), "copies": 5}))
+        return
+
+    if a.denoiser:
+        denoiser_bench(a)
         return
 
     from hilberta_amd.bridge_k import paired_plan_device

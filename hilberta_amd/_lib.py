@@ -37,6 +37,11 @@ SIGNATURES = {
     "hb_gather_rows": (
         _c_int, [_p, _p, _p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _p, _p],
     ),
+    "hb_qk_prep": (
+        _c_int,
+        [_p, _p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _p, _p, _c_f32, _p, _p, _p, _c_i64, _c_i64, _p],
+    ),
     "hb_hilbert_order": (_c_int, [_c_int, _p, _p]),
     "hb_plan_layout": (_c_int, [_c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p, _p, _p, _p, _p]),
     "hb_plan_scratch_bytes": (_c_i64, [_c_int, _c_int]),

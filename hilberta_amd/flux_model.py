@@ -1,0 +1,371 @@
+"""FLUX.1-dev-shaped denoiser transformer (random init) whose joint attention runs on the HIP path.
+
+The reference accelerates diffusers' FluxTransformer2DModel by replacing one operation per block
+(hilberta/flux_adapter.py:255-340, PersistentFluxProcessor) and by holding the image tokens in the
+persistent Hilbert layout for the whole transformer call (flux_adapter.py:149-252).  diffusers is
+not available here, so this module restates that transformer's structure (diffusers 0.36.0
+FluxTransformer2DModel with FLUX.1-dev's configuration) with random weights, to time one denoiser
+step at the real shapes:
+
+  * embedders: x (64 -> 3072), context (4096 -> 3072), timestep / guidance / pooled-text MLPs;
+  * 19 double-stream blocks: AdaLN-zero modulation per stream, QKV projections, per-head QK
+    RMSNorm, 3-axis RoPE (theta 10000, axes 16/56/56), joint [text; image] attention, output
+    projections, gated residuals, GELU(tanh) MLPs with ratio 4;
+  * 38 single-stream blocks over [text; image]: modulation, one fused QKV + MLP projection,
+    attention, concatenated output projection;
+  * AdaLN-continuous output norm and the 3072 -> 64 projection.
+
+The attention inputs are prepared by one HIP pass per tensor (flux_inputs.qk_prep: RMSNorm +
+rotation + concatenation straight into the [B, N, H, D] storage the kernels read).  Two attention
+modes:
+
+  * ``NativeAttention``: raster token order and dense attention on the same GPU (torch's
+    scaled_dot_product_attention, flash / memory-efficient backends) -- the "full attention"
+    comparison of the reference's denoiser rows;
+  * ``PersistentAttention``: image tokens and ids gathered into the plan's order once at entry,
+    block ``i`` of the 57 (double blocks first) attends with the plan's phase ``i % 4``
+    (flux_adapter.py:421, :269), the prediction gathered back to raster order once at exit
+    (flux_adapter.py:243).  Backends: ``paired`` (paired_kernel.paired_attention), ``sparse``
+    (sparse_kernel.sparse_attention on unpaired tables) and ``sdpa_reference`` (dense-mask SDPA,
+    a correctness reference as at flux_adapter.py:299-306).
+
+Weights and activations are bf16; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from .flux_inputs import qk_prep, rotary_tables
+from .layout import index_select_rows
+
+
+@dataclass(frozen=True)
+class FluxShape:
+    """FLUX.1-dev transformer hyper-parameters (diffusers FluxTransformer2DModel config)."""
+
+    num_layers: int = 19
+    num_single_layers: int = 38
+    heads: int = 24
+    head_dim: int = 128
+    mlp_ratio: float = 4.0
+    in_channels: int = 64
+    joint_attention_dim: int = 4096
+    pooled_projection_dim: int = 768
+    timestep_dim: int = 256
+    guidance_embeds: bool = True
+    eps: float = 1e-6
+
+    @property
+    def hidden(self):
+        return self.heads * self.head_dim
+
+    @property
+    def mlp_hidden(self):
+        return int(self.hidden * self.mlp_ratio)
+
+    @property
+    def blocks(self):
+        return self.num_layers + self.num_single_layers
+
+
+class _Init:
+    """Seeded random weights on the device: N(0, 1/fan_in) matrices, N(0, 0.02^2) biases, norm
+    weights around 1."""
+
+    def __init__(self, device, dtype, seed):
+        self.device, self.dtype = device, dtype
+        self.gen = torch.Generator(device=device)
+        self.gen.manual_seed(seed)
+
+    def linear(self, fan_out, fan_in, std=None):
+        w = torch.empty(fan_out, fan_in, device=self.device, dtype=self.dtype)
+        w.normal_(0.0, std if std is not None else fan_in**-0.5, generator=self.gen)
+        b = torch.empty(fan_out, device=self.device, dtype=self.dtype).normal_(0.0, 0.02, generator=self.gen)
+        return w, b
+
+    def norm(self, dim):
+        w = torch.empty(dim, device=self.device, dtype=self.dtype)
+        return w.normal_(1.0, 0.1, generator=self.gen)
+
+    def mlp(self, fan_in, hidden):
+        return self.linear(hidden, fan_in), self.linear(hidden, hidden)
+
+
+def timestep_projection(t, dim=256):
+    """diffusers get_timestep_embedding(flip_sin_to_cos=True, downscale_freq_shift=0): [cos | sin]
+    of t * 10000^(-j/half)."""
+    half = dim // 2
+    freqs = torch.exp(-math.log(10000) * torch.arange(half, dtype=torch.float32, device=t.device) / half)
+    angles = t[:, None].float() * freqs[None, :]
+    return torch.cat([angles.cos(), angles.sin()], dim=-1)
+
+
+def _mlp(x, layers):
+    (w1, b1), (w2, b2) = layers
+    return F.linear(F.silu(F.linear(x, w1, b1)), w2, b2)
+
+
+def _modulate(x, shift, scale, eps):
+    """LayerNorm without affine, then x * (1 + scale) + shift per batch row (AdaLN)."""
+    n = F.layer_norm(x, (x.shape[-1],), eps=eps)
+    return torch.addcmul(shift[:, None], n, (1 + scale)[:, None])
+
+
+class NativeAttention:
+    """Dense attention in raster order on the same GPU (the full-attention comparison)."""
+
+    layout = None
+
+    def __call__(self, layer, q, k, v, out):
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            out.copy_(F.scaled_dot_product_attention(q, k, v))
+
+
+class PersistentAttention:
+    """Persistent plan layout and per-block phase tables (flux_adapter.py:26-147, :255-340).
+
+    ``plan`` is either a ``bridge_k.DevicePlan`` (paired tables built on the GPU; ``paired`` only)
+    or an ``plan.AttentionPlan`` (from ``bridge_k_plan`` / ``build_plan``), whose tables are moved
+    to ``device`` once here and paired on the GPU.
+    """
+
+    BACKENDS = ("paired", "sparse", "sdpa_reference")
+
+    def __init__(self, plan, device, backend="paired", kernel_options=None):
+        from .bridge_k import DevicePlan
+        from .paired_metadata import pair_metadata_device
+        from .sparse_kernel import validate_metadata
+
+        if backend not in self.BACKENDS:
+            raise ValueError("backend must be paired/sparse/sdpa_reference")
+        self.backend = backend
+        self.kernel_options = dict(kernel_options or {})
+        self.global_tokens = plan.global_tokens
+        self.total_tokens = plan.total_tokens
+        self.calls = 0
+        if isinstance(plan, DevicePlan):
+            if backend != "paired":
+                raise ValueError("a DevicePlan carries paired tables only")
+            self.order = plan.layout.image_order.to(device)
+            self.inverse = plan.layout.inverse_image_order.to(device)
+            self.paired = list(plan.phases)
+            self.tables = None
+            self.plan = None
+        else:
+            self.order = plan.image_order.to(device=device, dtype=torch.int64)
+            self.inverse = plan.inverse_image_order.to(device=device, dtype=torch.int64)
+            cpu = [(p.kv_indices.cpu(), p.kv_counts.cpu()) for p in plan.phases]
+            for ids, counts in cpu:   # validated once, on the CPU, before they are cached on the GPU
+                validate_metadata(ids, counts, tokens=plan.total_tokens, global_tokens=plan.global_tokens,
+                                  block_size=plan.block_size)
+            if backend == "paired" and (plan.total_tokens % 128 or plan.global_tokens % 128):
+                raise ValueError("Paired queries require N/global aligned to 128; KV must be 64/128")
+            self.tables = [(ids.to(device), counts.to(device)) for ids, counts in cpu]
+            self.paired = [
+                pair_metadata_device(ids, counts, tokens=plan.total_tokens,
+                                     global_tokens=plan.global_tokens, device=device, validated=True)
+                for ids, counts in self.tables
+            ] if backend == "paired" else None
+            self.plan = plan
+            self.block_size = plan.block_size
+        self.masks = {}
+
+    layout = property(lambda self: self)
+
+    def __call__(self, layer, q, k, v, out):
+        phase = layer % 4
+        self.calls += 1
+        if self.backend == "paired":
+            from .paired_kernel import paired_attention
+
+            paired_attention(q, k, v, self.paired[phase], out=out, **self.kernel_options)
+        elif self.backend == "sparse":
+            from .sparse_kernel import sparse_attention
+
+            ids, counts = self.tables[phase]
+            sparse_attention(q, k, v, ids, counts, global_tokens=self.global_tokens,
+                             block_size=self.block_size, out=out, **self.kernel_options)
+        else:
+            if phase not in self.masks:
+                self.masks[phase] = self.plan.dense_mask(phase, q.device)
+            out.copy_(F.scaled_dot_product_attention(q, k, v, attn_mask=self.masks[phase]))
+
+
+class FluxTransformer:
+    """Random-init FLUX.1-dev-shaped transformer; ``forward`` is one denoiser evaluation."""
+
+    def __init__(self, device, shape: FluxShape = FluxShape(), *, seed=0, dtype=torch.bfloat16):
+        self.shape, self.device, self.dtype = shape, torch.device(device), dtype
+        s, C, M = shape, shape.hidden, shape.mlp_hidden
+        init = _Init(self.device, dtype, seed)
+        self.x_embedder = init.linear(C, s.in_channels)
+        self.context_embedder = init.linear(C, s.joint_attention_dim)
+        self.time_embedder = init.mlp(s.timestep_dim, C)
+        self.guidance_embedder = init.mlp(s.timestep_dim, C) if s.guidance_embeds else None
+        self.text_embedder = init.mlp(s.pooled_projection_dim, C)
+        # modulation weights are scaled down so the gated residual stream stays O(1) over 57 blocks
+        mod_std = 0.2 * C**-0.5
+        self.double = []
+        for _ in range(s.num_layers):
+            self.double.append(dict(
+                mod_x=init.linear(6 * C, C, mod_std), mod_c=init.linear(6 * C, C, mod_std),
+                qkv_x=init.linear(3 * C, C), qkv_c=init.linear(3 * C, C),
+                norm_q=init.norm(s.head_dim), norm_k=init.norm(s.head_dim),
+                norm_added_q=init.norm(s.head_dim), norm_added_k=init.norm(s.head_dim),
+                out_x=init.linear(C, C), out_c=init.linear(C, C),
+                ff_x=(init.linear(M, C), init.linear(C, M)), ff_c=(init.linear(M, C), init.linear(C, M)),
+            ))
+        self.single = []
+        for _ in range(s.num_single_layers):
+            self.single.append(dict(
+                mod=init.linear(3 * C, C, mod_std),
+                proj=init.linear(3 * C + M, C),          # to_q | to_k | to_v | proj_mlp
+                norm_q=init.norm(s.head_dim), norm_k=init.norm(s.head_dim),
+                proj_out=init.linear(C, C + M),
+            ))
+        self.norm_out = init.linear(2 * C, C, mod_std)
+        self.proj_out = init.linear(s.in_channels, C)
+
+    def parameters(self):
+        def walk(x):
+            if isinstance(x, torch.Tensor):
+                yield x
+            elif isinstance(x, (list, tuple)):
+                for y in x:
+                    yield from walk(y)
+            elif isinstance(x, dict):
+                for y in x.values():
+                    yield from walk(y)
+
+        for name in ("x_embedder", "context_embedder", "time_embedder", "guidance_embedder",
+                     "text_embedder", "double", "single", "norm_out", "proj_out"):
+            yield from walk(getattr(self, name))
+
+    def parameter_count(self):
+        return sum(p.numel() for p in self.parameters())
+
+    # ------------------------------------------------------------------ blocks
+    def _attend(self, attention, layer, q, k, v, out):
+        """q/k/v/out are [B, N, H, D] storages; the kernels read them as [B, H, N, D] views."""
+        attention(layer, q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), out.transpose(1, 2))
+
+    def _double_block(self, w, x, c, silu_t, cos, sin, attention, layer):
+        s, C, H = self.shape, self.shape.hidden, self.shape.heads
+        B, n, _ = x.shape
+        T = c.shape[1]
+        sx, scx, gx, sx2, scx2, gx2 = F.linear(silu_t, *w["mod_x"]).chunk(6, dim=1)
+        sc, scc, gc, sc2, scc2, gc2 = F.linear(silu_t, *w["mod_c"]).chunk(6, dim=1)
+        qkv_x = F.linear(_modulate(x, sx, scx, s.eps), *w["qkv_x"])
+        qkv_c = F.linear(_modulate(c, sc, scc, s.eps), *w["qkv_c"])
+        q = qk_prep(qkv_c[..., :C], qkv_x[..., :C], heads=H, weight_text=w["norm_added_q"],
+                    weight_image=w["norm_q"], eps=s.eps, cos=cos, sin=sin)
+        k = qk_prep(qkv_c[..., C:2 * C], qkv_x[..., C:2 * C], heads=H, weight_text=w["norm_added_k"],
+                    weight_image=w["norm_k"], eps=s.eps, cos=cos, sin=sin)
+        v = qk_prep(qkv_c[..., 2 * C:], qkv_x[..., 2 * C:], heads=H, normalize=False)
+        del qkv_x, qkv_c
+        o = torch.empty_like(q)
+        self._attend(attention, layer, q, k, v, o)
+        del q, k, v
+        o = o.view(B, T + n, C)
+        x = torch.addcmul(x, gx[:, None], F.linear(o[:, T:], *w["out_x"]))
+        c = torch.addcmul(c, gc[:, None], F.linear(o[:, :T], *w["out_c"]))
+        del o
+        for stream, shift, scale, gate, ff in ((0, sx2, scx2, gx2, w["ff_x"]), (1, sc2, scc2, gc2, w["ff_c"])):
+            h = x if stream == 0 else c
+            (w1, b1), (w2, b2) = ff
+            f = F.linear(F.gelu(F.linear(_modulate(h, shift, scale, s.eps), w1, b1), approximate="tanh"), w2, b2)
+            h = torch.addcmul(h, gate[:, None], f)
+            if stream == 0:
+                x = h
+            else:
+                c = h
+        return x, c
+
+    def _single_block(self, w, h, T, silu_t, cos, sin, attention, layer):
+        s, C, H, M = self.shape, self.shape.hidden, self.shape.heads, self.shape.mlp_hidden
+        B, N, _ = h.shape
+        shift, scale, gate = F.linear(silu_t, *w["mod"]).chunk(3, dim=1)
+        proj = F.linear(_modulate(h, shift, scale, s.eps), *w["proj"])       # [B, N, 3C + M]
+        q = qk_prep(proj[:, :T, :C], proj[:, T:, :C], heads=H, weight_text=w["norm_q"],
+                    weight_image=w["norm_q"], eps=s.eps, cos=cos, sin=sin)
+        k = qk_prep(proj[:, :T, C:2 * C], proj[:, T:, C:2 * C], heads=H, weight_text=w["norm_k"],
+                    weight_image=w["norm_k"], eps=s.eps, cos=cos, sin=sin)
+        v = proj[..., 2 * C:3 * C].unflatten(-1, (H, s.head_dim))
+        cat = torch.empty(B, N, C + M, device=h.device, dtype=h.dtype)       # [attention | mlp]
+        self._attend(attention, layer, q, k, v, cat[..., :C].unflatten(-1, (H, s.head_dim)))
+        del q, k
+        torch._C._nn.gelu(proj[..., 3 * C:], approximate="tanh", out=cat[..., C:])
+        del proj
+        return torch.addcmul(h, gate[:, None], F.linear(cat, *w["proj_out"]))
+
+    # ------------------------------------------------------------------ forward
+    def temb(self, timestep, guidance, pooled):
+        s = self.shape
+        t = timestep.to(self.dtype) * 1000
+        emb = _mlp(timestep_projection(t, s.timestep_dim).to(self.dtype), self.time_embedder)
+        if self.guidance_embedder is not None:
+            g = guidance.to(self.dtype) * 1000
+            emb = emb + _mlp(timestep_projection(g, s.timestep_dim).to(self.dtype), self.guidance_embedder)
+        return emb + _mlp(pooled.to(self.dtype), self.text_embedder)
+
+    @torch.inference_mode()
+    def forward(self, hidden_states, encoder_hidden_states, pooled_projections, timestep, img_ids,
+                txt_ids, guidance=None, *, attention=None):
+        """hidden_states [B, n, 64] packed latents (raster order), encoder_hidden_states
+        [B, T, 4096], pooled_projections [B, 768], timestep [B], img_ids [n, 3], txt_ids [T, 3]
+        -> predicted [B, n, 64] in raster order."""
+        s = self.shape
+        attention = attention if attention is not None else NativeAttention()
+        layout = attention.layout
+        B, n, _ = hidden_states.shape
+        T = encoder_hidden_states.shape[1]
+        if layout is not None:
+            if T + n != layout.total_tokens:
+                raise ValueError("token count does not match the plan")
+            hidden_states = index_select_rows(hidden_states, 1, layout.order)
+            img_ids = index_select_rows(img_ids.contiguous(), 0, layout.order)
+        cos, sin = rotary_tables(torch.cat([txt_ids, img_ids]).to(self.device))
+        silu_t = F.silu(self.temb(timestep, guidance, pooled_projections))
+        x = F.linear(hidden_states.to(self.dtype), *self.x_embedder)
+        c = F.linear(encoder_hidden_states.to(self.dtype), *self.context_embedder)
+        for i, w in enumerate(self.double):
+            x, c = self._double_block(w, x, c, silu_t, cos, sin, attention, i)
+        h = torch.cat([c, x], dim=1)
+        del x, c
+        for j, w in enumerate(self.single):
+            h = self._single_block(w, h, T, silu_t, cos, sin, attention, s.num_layers + j)
+        scale, shift = F.linear(silu_t, *self.norm_out).chunk(2, dim=1)
+        out = F.linear(_modulate(h[:, T:], shift, scale, s.eps), *self.proj_out)
+        if layout is not None:
+            out = index_select_rows(out, 1, layout.inverse)
+        return out
+
+    __call__ = forward
+
+
+def synthetic_inputs(device, *, grid, batch=1, text_tokens=512, shape: FluxShape = FluxShape(),
+                     seed=0, timestep=0.5, guidance=3.5):
+    """Seeded ~N(0,1) packed latents, text states and pooled embedding of FLUX's shapes, with the
+    pipeline's position ids (text zeros, image (0, row, col) in raster order)."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    n = grid * grid
+    r, c = torch.meshgrid(torch.arange(grid), torch.arange(grid), indexing="ij")
+    img_ids = torch.stack([torch.zeros(n), r.reshape(-1).float(), c.reshape(-1).float()], -1)
+    args = dict(
+        hidden_states=torch.randn(batch, n, shape.in_channels, generator=gen),
+        encoder_hidden_states=torch.randn(batch, text_tokens, shape.joint_attention_dim, generator=gen),
+        pooled_projections=torch.randn(batch, shape.pooled_projection_dim, generator=gen),
+        timestep=torch.full((batch,), timestep),
+        img_ids=img_ids,
+        txt_ids=torch.zeros(text_tokens, 3),
+        guidance=torch.full((batch,), guidance),
+    )
+    return {k: v.to(device=device, dtype=torch.bfloat16 if v.dtype == torch.float32 and v.ndim == 3 else v.dtype)
+            for k, v in args.items()}

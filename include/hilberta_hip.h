@@ -78,6 +78,23 @@ int hb_gather_rows(const void* src, void* dst, const int64_t* index, int64_t row
                    int64_t dst_row_stride, int64_t row_bytes, int64_t src_rows, int32_t* error,
                    hb_stream_t stream);
 
+/* ---------------------------------------------------------------- FLUX attention inputs
+ * Per-head RMSNorm + rotary embedding + [text; image] concatenation into one BNHD tensor
+ * out[b, t, h, :] (head_dim 128).  Replaces, at reference hilberta/flux_adapter.py:283-295,
+ * attn.norm_q/norm_k/norm_added_q/norm_added_k (diffusers 0.36.0 RMSNorm), the torch.cat of text
+ * and image tokens and apply_rotary_emb (use_real, interleaved pairs).  Tokens t < text_tokens
+ * are read from src_text row t with weight_text, the others from src_image row t - text_tokens
+ * with weight_image (element strides; rows hold heads*128 elements).  normalize=0 skips the
+ * RMSNorm (weights must then be NULL); cos = sin = NULL skips the rotation; cos/sin are fp32
+ * [tokens, 128] rows in output token order.  All pointers 16-byte aligned, strides multiples
+ * of 8.  An in-place call (out aliasing a source) is not allowed. */
+int hb_qk_prep(const void* src_text, const void* src_image, int64_t text_batch_stride,
+               int64_t text_row_stride, int64_t image_batch_stride, int64_t image_row_stride,
+               int32_t batch, int32_t text_tokens, int32_t tokens, int32_t heads, int32_t head_dim,
+               int32_t dtype, int32_t normalize, const void* weight_text,
+               const void* weight_image, float eps, const float* cos, const float* sin, void* out,
+               int64_t out_batch_stride, int64_t out_row_stride, hb_stream_t stream);
+
 /* ---------------------------------------------------------------- (b) block tables
  * Hilbert order of a grid_size x grid_size raster (reference hilberta/geometry.py:6-25). */
 int hb_hilbert_order(int32_t grid_size, int64_t* out, hb_stream_t stream);
