@@ -136,6 +136,43 @@ def cpu_baseline(q, k, v, meta_phase0, budget_s):
 REFERENCE_DENOISER_MS = {1024: (208.473, 179.918, 177.075), 2048: (1150.413, 712.444, 639.542)}
 
 
+def denoiser_kernels(dev, stream, N, shape):
+    """The denoiser's own HBM-bound HIP kernels at the step's shape (B=1): Q+K prep of a fused
+    [N, 3C] projection, and the gated residual + AdaLN of [N, C] rows.  Algorithmic bytes: each
+    kernel reads and writes every element once (2 bytes each); the prep's fp32 cos/sin rows
+    (N x 128 x 8 bytes) are counted once."""
+    from hilberta_amd.flux_inputs import qk_prep_pair, rotary_tables
+    from hilberta_amd.flux_norm import adaln_modulate
+
+    C, H, T = shape.hidden, shape.heads, 512
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    qkv = torch.randn(1, N, 3 * C, device=dev, generator=gen).to(torch.bfloat16)
+    ids = torch.zeros(N, 3, device=dev)
+    ids[T:, 1] = torch.arange(N - T, device=dev) // 128
+    ids[T:, 2] = torch.arange(N - T, device=dev) % 128
+    cos, sin = rotary_tables(ids)
+    w = torch.ones(4, 128, device=dev, dtype=torch.bfloat16)
+    out = torch.empty(2, 1, N, H, 128, device=dev, dtype=torch.bfloat16)
+    prep = lambda: qk_prep_pair(qkv[:, :T, :2 * C], qkv[:, T:, :2 * C], heads=H, out=out,  # noqa: E731
+                                weights=((w[0], w[1]), (w[2], w[3])), cos=cos, sin=sin)
+    x = torch.randn(1, N, C, device=dev, generator=gen).to(torch.bfloat16)
+    y = torch.randn(1, N, C, device=dev, generator=gen).to(torch.bfloat16)
+    mod = torch.randn(1, 3 * C, device=dev, generator=gen).to(torch.bfloat16) * 0.1
+    xn = torch.empty_like(x)
+    ada = lambda: adaln_modulate(x, mod[:, :C], mod[:, C:2 * C], y=y, gate=mod[:, 2 * C:],  # noqa: E731
+                                 x_out=x, out=xn)
+    res = {}
+    for name, fn, nbytes in (("qk_prep_pair", prep, 2 * 2 * N * C * 2 + N * 128 * 8),
+                             ("adaln_modulate", ada, 4 * N * C * 2)):
+        for _ in range(3):
+            fn()
+        us = statistics.median(event_time(fn, 20, stream)) * 1e3
+        res[name] = dict(us=round(us, 1), bytes=nbytes, GBps=round(nbytes / (us * 1e-6) / 1e9, 1),
+                         hbm_frac=round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 3))
+    return res
+
+
 def denoiser_bench(a):
     """One FLUX-shaped denoiser forward, full attention vs the paired HIP kernel (see --denoiser)."""
     from hilberta_amd.bridge_k import paired_plan_device
@@ -150,11 +187,15 @@ def denoiser_bench(a):
     log(f"denoiser {a.denoiser}px: building the random-init model ...")
     model = FluxTransformer(dev, shape, seed=0)
     args = synthetic_inputs(dev, grid=grid, batch=a.batch, shape=shape, seed=2707)
-    modes = {"full": NativeAttention()}
+    wanted = a.modes.split(",")
+    if not set(wanted) <= {"full", "t4k1", "t16k3"}:
+        raise SystemExit("--modes takes a subset of full,t4k1,t16k3")
+    modes = {"full": NativeAttention()} if "full" in wanted else {}
     for tiles, k in ((4, 1), (16, 3)):
-        plan = paired_plan_device(tiles, k, grid_size=grid, device=dev)
-        modes[f"t{tiles}k{k}"] = PersistentAttention(plan, dev, "paired",
-                                                     dict(global_strategy="triton", num_warps=8))
+        if f"t{tiles}k{k}" in wanted:
+            plan = paired_plan_device(tiles, k, grid_size=grid, device=dev)
+            modes[f"t{tiles}k{k}"] = PersistentAttention(plan, dev, "paired",
+                                                         dict(global_strategy="triton", num_warps=8))
     steps = max(1, min(a.steps, 10))
     warmup = max(1, min(a.warmup, 3))
     ms, outputs = {}, {}
@@ -168,19 +209,24 @@ def denoiser_bench(a):
         log(f"  {name}: {ms[name]:.2f} ms (median of {steps})")
     wall_ms = (time.perf_counter() - t_start) * 1e3
     finite = all(bool(torch.isfinite(o).all()) for o in outputs.values())
-    ref = outputs["full"].float()
-    rel = {name: round(float((o.float() - ref).norm() / ref.norm()), 4)
-           for name, o in outputs.items() if name != "full"}
+    rel = {}
+    if "full" in outputs:
+        ref = outputs["full"].float()
+        rel = {name: round(float((o.float() - ref).norm() / ref.norm()), 4)
+               for name, o in outputs.items() if name != "full"}
+    head = "t16k3" if "t16k3" in ms else next(iter(ms))
     n_img = grid * grid
+    kernels = denoiser_kernels(dev, stream, 512 + n_img, shape)
     result = {
         "metric": f"FLUX-shaped denoiser step ms at {a.denoiser}px, paired HIP sparse attn (16-tile K3) "
         "vs full attn",
-        "value": round(ms["t16k3"], 2),
+        "value": round(ms[head], 2),
+        "value_mode": head,
         "unit": "ms",
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
-        "ms_per_step": round(ms["t16k3"], 2),
+        "ms_per_step": round(ms[head], 2),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -195,11 +241,13 @@ def denoiser_bench(a):
             "parallelism": "single GPU",
         },
         "denoiser_ms": {name: round(t, 2) for name, t in ms.items()},
-        "speedup_vs_full": {name: round(ms["full"] / t, 3) for name, t in ms.items() if name != "full"},
+        "speedup_vs_full": {name: round(ms["full"] / t, 3) for name, t in ms.items()
+                            if name != "full" and "full" in ms},
         "reference_h100_ms": dict(zip(("full", "t4k1", "t16k3"), REFERENCE_DENOISER_MS[a.denoiser])),
         "relative_l2_vs_full": rel,
         "finite": finite,
         "parameters": model.parameter_count(),
+        "kernels": kernels,
         "timed_wall_ms": round(wall_ms, 1),
     }
     print(json.dumps(result), flush=True)
@@ -217,6 +265,8 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="attention only (for counter runs)")
     ap.add_argument("--denoiser", type=int, choices=(1024, 2048), default=0, metavar="PX",
                     help="time one FLUX-shaped denoiser step at PX (1024 or 2048) instead")
+    ap.add_argument("--modes", default="full,t4k1,t16k3",
+                    help="denoiser attention modes to time (comma-separated subset of full,t4k1,t16k3)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 5 times (calibrates FETCH/WRITE_SIZE)")
     a = ap.parse_args()

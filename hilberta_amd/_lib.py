@@ -39,8 +39,13 @@ SIGNATURES = {
     ),
     "hb_qk_prep": (
         _c_int,
-        [_p, _p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
-         _c_int, _p, _p, _c_f32, _p, _p, _p, _c_i64, _c_i64, _p],
+        [_p, _p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_int, _c_int, _p, _c_f32, _p, _p, _p, _c_i64, _c_i64, _c_i64, _p],
+    ),
+    "hb_adaln_modulate": (
+        _c_int,
+        [_c_int, _c_int, _c_int, _c_int, _c_f32, _p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _c_i64,
+         _p, _c_i64, _c_i64, _p, _p, _c_i64, _p, _c_i64, _c_i64, _p],
     ),
     "hb_hilbert_order": (_c_int, [_c_int, _p, _p]),
     "hb_plan_layout": (_c_int, [_c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p, _p, _p, _p, _p]),

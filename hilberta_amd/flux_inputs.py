@@ -14,6 +14,8 @@ in the order the tokens are stored, e.g. after the persistent Hilbert permutatio
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -42,37 +44,32 @@ def rotary_tables(ids, theta=THETA, axes_dim=AXES_DIM):
 
 def _rows(x, name):
     if x.ndim != 3 or x.stride(-1) != 1:
-        raise ValueError(f"{name} must be [B, tokens, heads*128] with a contiguous last dimension")
+        raise ValueError(f"{name} must be [B, tokens, columns] with a contiguous last dimension")
     return x.stride(0), x.stride(1)
 
 
-def qk_prep(text, image, *, heads, out=None, normalize=True, weight_text=None, weight_image=None,
-            eps=1e-6, cos=None, sin=None):
-    """[text; image] tokens -> out [B, T+n, heads, 128], with per-head RMSNorm (weights optional)
-    when ``normalize`` and the rotation when ``cos``/``sin`` are given.
-
-    ``text`` [B, T, heads*128] and ``image`` [B, n, heads*128] may be column slices of a fused
-    projection (row stride > heads*128).  ``text`` may be None when T = 0.
-    """
+def _launch(text, image, *, heads, planes, out, out_plane_stride, normalize, weights, eps, cos, sin):
     _lib.require_gpu(image)
-    B, n, width = image.shape if image.ndim == 3 else (None, None, None)
-    if width != heads * HEAD_DIM:
-        raise ValueError("image must be [B, n, heads*128]")
+    width = planes * heads * HEAD_DIM
+    if image.ndim != 3 or image.shape[2] != width:
+        raise ValueError(f"image must be [B, n, {planes}*heads*128]")
+    B, n = image.shape[:2]
     T = 0 if text is None else text.shape[1]
     if text is not None:
         _lib.require_gpu(text)
         if text.ndim != 3 or text.shape[0] != B or text.shape[2] != width or text.dtype != image.dtype:
-            raise ValueError("text must be [B, T, heads*128] with image's batch and dtype")
+            raise ValueError("text must be [B, T, columns] with image's batch, columns and dtype")
     if image.dtype not in _DTYPES:
         raise ValueError("Q/K/V projections must be bf16 or fp16")
     N = T + n
-    if out is None:
-        out = torch.empty(B, N, heads, HEAD_DIM, dtype=image.dtype, device=image.device)
-    elif (out.shape != (B, N, heads, HEAD_DIM) or out.dtype != image.dtype
-          or out.stride(3) != 1 or out.stride(2) != HEAD_DIM):
-        raise ValueError("out must be [B, N, heads, 128] with contiguous heads")
+    plane_shape = (B, N, heads, HEAD_DIM)
+    views = [out] if planes == 1 else [out[0], out[1]]
+    for o in views:
+        if o.shape != plane_shape or o.dtype != image.dtype or o.stride(3) != 1 or o.stride(2) != HEAD_DIM:
+            raise ValueError("out must be [B, N, heads, 128] per plane with contiguous heads")
     tensors = [image, out] + ([text] if text is not None else [])
-    for w in (weight_text, weight_image):
+    flat = [w for pair in weights for w in pair]
+    for w in flat:
         if w is not None:
             if not normalize or w.shape != (HEAD_DIM,) or w.dtype != image.dtype or not w.is_contiguous():
                 raise ValueError("norm weights are contiguous [128] tensors in the input dtype")
@@ -89,10 +86,48 @@ def qk_prep(text, image, *, heads, out=None, normalize=True, weight_text=None, w
     tb, tr = _rows(text, "text") if text is not None else (0, 0)
     ib, ir = _rows(image, "image")
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    warr = (ctypes.c_void_p * 4)(*[ptr(w) for w in flat], *([None] * (4 - len(flat))))
+    o0 = views[0]
     rc = _lib.load().hb_qk_prep(
-        ptr(text), image.data_ptr(), tb, tr, ib, ir, B, T, N, heads, HEAD_DIM, _DTYPES[image.dtype],
-        int(bool(normalize)), ptr(weight_text), ptr(weight_image), float(eps), ptr(cos), ptr(sin),
-        out.data_ptr(), out.stride(0), out.stride(1), _lib.stream_ptr(image.device),
+        ptr(text), image.data_ptr(), tb, tr, ib, ir, planes, heads * HEAD_DIM, B, T, N, heads,
+        HEAD_DIM, _DTYPES[image.dtype], int(bool(normalize)), warr, float(eps), ptr(cos), ptr(sin),
+        o0.data_ptr(), out_plane_stride, o0.stride(0), o0.stride(1), _lib.stream_ptr(image.device),
     )
     _lib.check(rc, "hb_qk_prep")
     return out
+
+
+def _new_out(planes, text, image, heads):
+    B, n = image.shape[:2]
+    N = n + (0 if text is None else text.shape[1])
+    shape = (B, N, heads, HEAD_DIM) if planes == 1 else (2, B, N, heads, HEAD_DIM)
+    return torch.empty(shape, dtype=image.dtype, device=image.device)
+
+
+def qk_prep(text, image, *, heads, out=None, normalize=True, weight_text=None, weight_image=None,
+            eps=1e-6, cos=None, sin=None):
+    """[text; image] tokens -> out [B, T+n, heads, 128], with per-head RMSNorm (weights optional)
+    when ``normalize`` and the rotation when ``cos``/``sin`` are given.
+
+    ``text`` [B, T, heads*128] and ``image`` [B, n, heads*128] may be column slices of a fused
+    projection (row stride > heads*128) or row ranges of one tensor.  ``text`` may be None (T = 0).
+    """
+    if out is None:
+        out = _new_out(1, text, image, heads)
+    return _launch(text, image, heads=heads, planes=1, out=out, out_plane_stride=0,
+                   normalize=normalize, weights=((weight_text, weight_image),), eps=eps, cos=cos,
+                   sin=sin)
+
+
+def qk_prep_pair(text, image, *, heads, out=None, weights=((None, None), (None, None)), eps=1e-6,
+                 cos=None, sin=None):
+    """Q and K in one launch: ``text`` / ``image`` hold the Q columns then the K columns
+    ([B, T or n, 2*heads*128], e.g. a slice of a fused QKV projection); both are RMS-normalised
+    with ``weights`` = ((q_text, q_image), (k_text, k_image)) and rotated.  Returns out
+    [2, B, N, heads, 128] (out[0] = Q, out[1] = K)."""
+    if out is None:
+        out = _new_out(2, text, image, heads)
+    if out.ndim != 5 or out.shape[0] != 2:
+        raise ValueError("out must be [2, B, N, heads, 128]")
+    return _launch(text, image, heads=heads, planes=2, out=out, out_plane_stride=out.stride(0),
+                   normalize=True, weights=weights, eps=eps, cos=cos, sin=sin)

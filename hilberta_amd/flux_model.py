@@ -15,9 +15,10 @@ step at the real shapes:
     attention, concatenated output projection;
   * AdaLN-continuous output norm and the 3072 -> 64 projection.
 
-The attention inputs are prepared by one HIP pass per tensor (flux_inputs.qk_prep: RMSNorm +
-rotation + concatenation straight into the [B, N, H, D] storage the kernels read).  Two attention
-modes:
+Q and K are prepared by one HIP pass (flux_inputs.qk_prep_pair: RMSNorm + rotation +
+[text; image] concatenation straight into the [B, N, H, D] storage the kernels read), V is read in
+place from the joint QKV projection, and every gated residual add is fused with the next AdaLN
+modulation (flux_norm.adaln_modulate).  Two attention modes:
 
   * ``NativeAttention``: raster token order and dense attention on the same GPU (torch's
     scaled_dot_product_attention, flash / memory-efficient backends) -- the "full attention"
@@ -40,7 +41,8 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from .flux_inputs import qk_prep, rotary_tables
+from .flux_inputs import qk_prep_pair, rotary_tables
+from .flux_norm import adaln_modulate
 from .layout import index_select_rows
 
 
@@ -82,10 +84,16 @@ class _Init:
         self.gen = torch.Generator(device=device)
         self.gen.manual_seed(seed)
 
-    def linear(self, fan_out, fan_in, std=None):
-        w = torch.empty(fan_out, fan_in, device=self.device, dtype=self.dtype)
+    def linear(self, fan_out, fan_in, std=None, *, out_features=None, in_features=None, bias=True):
+        """(weight [out_features, in_features], bias) with N(0, std^2), std defaulting to
+        fan_in^-0.5; the feature counts default to fan_out / fan_in (a column block of a larger
+        layer passes its own)."""
+        shape = (out_features or fan_out, in_features or fan_in)
+        w = torch.empty(shape, device=self.device, dtype=self.dtype)
         w.normal_(0.0, std if std is not None else fan_in**-0.5, generator=self.gen)
-        b = torch.empty(fan_out, device=self.device, dtype=self.dtype).normal_(0.0, 0.02, generator=self.gen)
+        if not bias:
+            return w, None
+        b = torch.empty(shape[0], device=self.device, dtype=self.dtype).normal_(0.0, 0.02, generator=self.gen)
         return w, b
 
     def norm(self, dim):
@@ -108,12 +116,6 @@ def timestep_projection(t, dim=256):
 def _mlp(x, layers):
     (w1, b1), (w2, b2) = layers
     return F.linear(F.silu(F.linear(x, w1, b1)), w2, b2)
-
-
-def _modulate(x, shift, scale, eps):
-    """LayerNorm without affine, then x * (1 + scale) + shift per batch row (AdaLN)."""
-    n = F.layer_norm(x, (x.shape[-1],), eps=eps)
-    return torch.addcmul(shift[:, None], n, (1 + scale)[:, None])
 
 
 class NativeAttention:
@@ -198,8 +200,31 @@ class PersistentAttention:
             out.copy_(F.scaled_dot_product_attention(q, k, v, attn_mask=self.masks[phase]))
 
 
+def _linear_into(x, weight, bias, out):
+    """out[b] = x[b] @ weight^T + bias for every batch row, written in place (out may be a row
+    range of a larger buffer: one GEMM per batch element writes straight into it)."""
+    for b in range(x.shape[0]):
+        torch.addmm(bias, x[b], weight.t(), out=out[b])
+
+
+def _gelu_linear(x, weight, bias):
+    """GELU(tanh)(x @ weight^T + bias) with the activation in the GEMM epilogue."""
+    flat = x.reshape(-1, x.shape[-1])
+    return torch._addmm_activation(bias, flat, weight.t(), use_gelu=True).view(*x.shape[:-1], -1)
+
+
 class FluxTransformer:
-    """Random-init FLUX.1-dev-shaped transformer; ``forward`` is one denoiser evaluation."""
+    """Random-init FLUX.1-dev-shaped transformer; ``forward`` is one denoiser evaluation.
+
+    Fused where the HIP path allows it, with the same arithmetic as the diffusers blocks up to
+    rounding order: the text and image QKV projections of a double block write one joint
+    [B, N, 3C] buffer (V is read from it in place), Q and K are normalised and rotated by one
+    qk_prep_pair launch, every gated residual add is fused with the following AdaLN modulation
+    (flux_norm.adaln_modulate; all blocks' modulation vectors depend only on the timestep
+    embedding and are computed up front), the MLP GELU runs in the GEMM epilogue, and the single
+    blocks' output projection over [attention | mlp] is two accumulating GEMMs instead of a
+    concatenation.
+    """
 
     def __init__(self, device, shape: FluxShape = FluxShape(), *, seed=0, dtype=torch.bfloat16):
         self.shape, self.device, self.dtype = shape, torch.device(device), dtype
@@ -223,12 +248,15 @@ class FluxTransformer:
                 ff_x=(init.linear(M, C), init.linear(C, M)), ff_c=(init.linear(M, C), init.linear(C, M)),
             ))
         self.single = []
+        out_std = (C + M) ** -0.5
         for _ in range(s.num_single_layers):
             self.single.append(dict(
                 mod=init.linear(3 * C, C, mod_std),
-                proj=init.linear(3 * C + M, C),          # to_q | to_k | to_v | proj_mlp
+                qkv=init.linear(3 * C, C),                       # to_q | to_k | to_v
+                mlp=init.linear(M, C),                           # proj_mlp
                 norm_q=init.norm(s.head_dim), norm_k=init.norm(s.head_dim),
-                proj_out=init.linear(C, C + M),
+                out_attn=init.linear(C, C + M, out_std, out_features=C, in_features=C),
+                out_mlp=init.linear(C, C + M, out_std, out_features=C, in_features=M, bias=False),
             ))
         self.norm_out = init.linear(2 * C, C, mod_std)
         self.proj_out = init.linear(s.in_channels, C)
@@ -249,61 +277,86 @@ class FluxTransformer:
             yield from walk(getattr(self, name))
 
     def parameter_count(self):
-        return sum(p.numel() for p in self.parameters())
+        return sum(p.numel() for p in self.parameters() if p is not None)
 
     # ------------------------------------------------------------------ blocks
     def _attend(self, attention, layer, q, k, v, out):
         """q/k/v/out are [B, N, H, D] storages; the kernels read them as [B, H, N, D] views."""
         attention(layer, q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), out.transpose(1, 2))
 
-    def _double_block(self, w, x, c, silu_t, cos, sin, attention, layer):
+    def _modulations(self, silu_t):
+        """Every block's AdaLN vectors (they depend on the timestep embedding only)."""
+        double = [(F.linear(silu_t, *w["mod_x"]).chunk(6, dim=1), F.linear(silu_t, *w["mod_c"]).chunk(6, dim=1))
+                  for w in self.double]
+        single = [F.linear(silu_t, *w["mod"]).chunk(3, dim=1) for w in self.single]
+        scale, shift = F.linear(silu_t, *self.norm_out).chunk(2, dim=1)   # AdaLayerNormContinuous order
+        return double, single, (shift, scale)
+
+    def _double_block(self, w, mods, x, xn, c, cn, cos, sin, attention, layer, next_mods, joint_out):
+        """One double-stream block.  x / c are the residual streams, xn / cn their modulated rows
+        (produced by the previous fused step).  Returns the updated (x, xn, c, cn); the residual
+        add after the MLP is fused with the next block's modulation ``next_mods`` (shift, scale)
+        pairs for image and text, or written into ``joint_out`` = (h, hn) [B, N, C] buffers when
+        this is the last double block."""
         s, C, H = self.shape, self.shape.hidden, self.shape.heads
         B, n, _ = x.shape
         T = c.shape[1]
-        sx, scx, gx, sx2, scx2, gx2 = F.linear(silu_t, *w["mod_x"]).chunk(6, dim=1)
-        sc, scc, gc, sc2, scc2, gc2 = F.linear(silu_t, *w["mod_c"]).chunk(6, dim=1)
-        qkv_x = F.linear(_modulate(x, sx, scx, s.eps), *w["qkv_x"])
-        qkv_c = F.linear(_modulate(c, sc, scc, s.eps), *w["qkv_c"])
-        q = qk_prep(qkv_c[..., :C], qkv_x[..., :C], heads=H, weight_text=w["norm_added_q"],
-                    weight_image=w["norm_q"], eps=s.eps, cos=cos, sin=sin)
-        k = qk_prep(qkv_c[..., C:2 * C], qkv_x[..., C:2 * C], heads=H, weight_text=w["norm_added_k"],
-                    weight_image=w["norm_k"], eps=s.eps, cos=cos, sin=sin)
-        v = qk_prep(qkv_c[..., 2 * C:], qkv_x[..., 2 * C:], heads=H, normalize=False)
-        del qkv_x, qkv_c
-        o = torch.empty_like(q)
-        self._attend(attention, layer, q, k, v, o)
-        del q, k, v
+        (sx, scx, gx, sx2, scx2, gx2), (sc, scc, gc, sc2, scc2, gc2) = mods
+        qkv = torch.empty(B, T + n, 3 * C, device=x.device, dtype=x.dtype)
+        _linear_into(cn, *w["qkv_c"], qkv[:, :T])
+        _linear_into(xn, *w["qkv_x"], qkv[:, T:])
+        qk = qk_prep_pair(qkv[:, :T, :2 * C], qkv[:, T:, :2 * C], heads=H, eps=s.eps, cos=cos, sin=sin,
+                          weights=((w["norm_added_q"], w["norm_q"]), (w["norm_added_k"], w["norm_k"])))
+        v = qkv[..., 2 * C:].unflatten(-1, (H, s.head_dim))
+        o = torch.empty_like(qk[0])
+        self._attend(attention, layer, qk[0], qk[1], v, o)
+        del qk, v, qkv
         o = o.view(B, T + n, C)
-        x = torch.addcmul(x, gx[:, None], F.linear(o[:, T:], *w["out_x"]))
-        c = torch.addcmul(c, gc[:, None], F.linear(o[:, :T], *w["out_c"]))
+        ax = F.linear(o[:, T:], *w["out_x"])
+        ac = F.linear(o[:, :T], *w["out_c"])
         del o
-        for stream, shift, scale, gate, ff in ((0, sx2, scx2, gx2, w["ff_x"]), (1, sc2, scc2, gc2, w["ff_c"])):
-            h = x if stream == 0 else c
-            (w1, b1), (w2, b2) = ff
-            f = F.linear(F.gelu(F.linear(_modulate(h, shift, scale, s.eps), w1, b1), approximate="tanh"), w2, b2)
-            h = torch.addcmul(h, gate[:, None], f)
-            if stream == 0:
-                x = h
-            else:
-                c = h
-        return x, c
+        xn = adaln_modulate(x, sx2, scx2, y=ax, gate=gx, x_out=x, eps=s.eps)
+        cn = adaln_modulate(c, sc2, scc2, y=ac, gate=gc, x_out=c, eps=s.eps)
+        del ax, ac
+        (w1, b1), (w2, b2) = w["ff_x"]
+        fx = F.linear(_gelu_linear(xn, w1, b1), w2, b2)
+        (w1, b1), (w2, b2) = w["ff_c"]
+        fc = F.linear(_gelu_linear(cn, w1, b1), w2, b2)
+        if joint_out is None:
+            (nsx, nscx), (nsc, nscc) = next_mods
+            xn = adaln_modulate(x, nsx, nscx, y=fx, gate=gx2, x_out=x, eps=s.eps)
+            cn = adaln_modulate(c, nsc, nscc, y=fc, gate=gc2, x_out=c, eps=s.eps)
+            return x, xn, c, cn
+        h, hn = joint_out
+        nshift, nscale = next_mods
+        adaln_modulate(x, nshift, nscale, y=fx, gate=gx2, x_out=h[:, T:], out=hn[:, T:], eps=s.eps)
+        adaln_modulate(c, nshift, nscale, y=fc, gate=gc2, x_out=h[:, :T], out=hn[:, :T], eps=s.eps)
+        return None
 
-    def _single_block(self, w, h, T, silu_t, cos, sin, attention, layer):
-        s, C, H, M = self.shape, self.shape.hidden, self.shape.heads, self.shape.mlp_hidden
+    def _single_block(self, w, mods, h, hn, T, cos, sin, attention, layer, next_mods):
+        """One single-stream block over [text; image].  Returns (h, hn) with the residual add
+        fused with the next block's modulation, or, for the last block, the image rows modulated
+        by the output norm (``next_mods`` = norm_out's (shift, scale)) and no residual."""
+        s, C, H = self.shape, self.shape.hidden, self.shape.heads
         B, N, _ = h.shape
-        shift, scale, gate = F.linear(silu_t, *w["mod"]).chunk(3, dim=1)
-        proj = F.linear(_modulate(h, shift, scale, s.eps), *w["proj"])       # [B, N, 3C + M]
-        q = qk_prep(proj[:, :T, :C], proj[:, T:, :C], heads=H, weight_text=w["norm_q"],
-                    weight_image=w["norm_q"], eps=s.eps, cos=cos, sin=sin)
-        k = qk_prep(proj[:, :T, C:2 * C], proj[:, T:, C:2 * C], heads=H, weight_text=w["norm_k"],
-                    weight_image=w["norm_k"], eps=s.eps, cos=cos, sin=sin)
-        v = proj[..., 2 * C:3 * C].unflatten(-1, (H, s.head_dim))
-        cat = torch.empty(B, N, C + M, device=h.device, dtype=h.dtype)       # [attention | mlp]
-        self._attend(attention, layer, q, k, v, cat[..., :C].unflatten(-1, (H, s.head_dim)))
-        del q, k
-        torch._C._nn.gelu(proj[..., 3 * C:], approximate="tanh", out=cat[..., C:])
-        del proj
-        return torch.addcmul(h, gate[:, None], F.linear(cat, *w["proj_out"]))
+        _, _, gate = mods
+        qkv = F.linear(hn, *w["qkv"])                                      # [B, N, 3C]
+        mlp = _gelu_linear(hn, *w["mlp"])                                  # [B, N, M]
+        qk = qk_prep_pair(qkv[:, :T, :2 * C], qkv[:, T:, :2 * C], heads=H, eps=s.eps, cos=cos, sin=sin,
+                          weights=((w["norm_q"], w["norm_q"]), (w["norm_k"], w["norm_k"])))
+        v = qkv[..., 2 * C:].unflatten(-1, (H, s.head_dim))
+        o = torch.empty_like(qk[0])
+        self._attend(attention, layer, qk[0], qk[1], v, o)
+        del qk, v, qkv
+        (wa, ba), (wm, _) = w["out_attn"], w["out_mlp"]
+        p = torch.addmm(ba, o.view(B * N, C), wa.t())
+        p = torch.addmm(p, mlp.view(B * N, -1), wm.t()).view(B, N, C)
+        del o, mlp
+        shift, scale = next_mods
+        if layer < self.shape.blocks - 1:
+            hn = adaln_modulate(h, shift, scale, y=p, gate=gate, x_out=h, eps=s.eps)
+            return h, hn
+        return None, adaln_modulate(h[:, T:], shift, scale, y=p[:, T:], gate=gate, eps=s.eps)
 
     # ------------------------------------------------------------------ forward
     def temb(self, timestep, guidance, pooled):
@@ -326,23 +379,39 @@ class FluxTransformer:
         layout = attention.layout
         B, n, _ = hidden_states.shape
         T = encoder_hidden_states.shape[1]
+        N = T + n
         if layout is not None:
-            if T + n != layout.total_tokens:
+            if N != layout.total_tokens:
                 raise ValueError("token count does not match the plan")
             hidden_states = index_select_rows(hidden_states, 1, layout.order)
             img_ids = index_select_rows(img_ids.contiguous(), 0, layout.order)
         cos, sin = rotary_tables(torch.cat([txt_ids, img_ids]).to(self.device))
-        silu_t = F.silu(self.temb(timestep, guidance, pooled_projections))
+        double_mods, single_mods, out_mods = self._modulations(F.silu(self.temb(timestep, guidance,
+                                                                                pooled_projections)))
         x = F.linear(hidden_states.to(self.dtype), *self.x_embedder)
         c = F.linear(encoder_hidden_states.to(self.dtype), *self.context_embedder)
+        (sx, scx, *_), (sc, scc, *_) = double_mods[0]
+        xn = adaln_modulate(x, sx, scx, eps=s.eps)
+        cn = adaln_modulate(c, sc, scc, eps=s.eps)
+        h = torch.empty(B, N, s.hidden, device=x.device, dtype=x.dtype)
+        hn = torch.empty_like(h)
         for i, w in enumerate(self.double):
-            x, c = self._double_block(w, x, c, silu_t, cos, sin, attention, i)
-        h = torch.cat([c, x], dim=1)
-        del x, c
+            last = i == len(self.double) - 1
+            if last:
+                nxt = single_mods[0][:2] if self.single else out_mods
+                self._double_block(w, double_mods[i], x, xn, c, cn, cos, sin, attention, i, nxt, (h, hn))
+            else:
+                (nsx, nscx, *_), (nsc, nscc, *_) = double_mods[i + 1]
+                x, xn, c, cn = self._double_block(w, double_mods[i], x, xn, c, cn, cos, sin, attention, i,
+                                                  ((nsx, nscx), (nsc, nscc)), None)
+        del x, xn, c, cn
         for j, w in enumerate(self.single):
-            h = self._single_block(w, h, T, silu_t, cos, sin, attention, s.num_layers + j)
-        scale, shift = F.linear(silu_t, *self.norm_out).chunk(2, dim=1)
-        out = F.linear(_modulate(h[:, T:], shift, scale, s.eps), *self.proj_out)
+            nxt = single_mods[j + 1][:2] if j + 1 < len(self.single) else out_mods
+            h, hn = self._single_block(w, single_mods[j], h, hn, T, cos, sin, attention,
+                                       s.num_layers + j, nxt)
+        if hn.shape[1] != n:   # no single blocks: the last double block modulated every row
+            hn = hn[:, T:]
+        out = F.linear(hn, *self.proj_out)
         if layout is not None:
             out = index_select_rows(out, 1, layout.inverse)
         return out

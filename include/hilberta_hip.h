@@ -83,17 +83,42 @@ int hb_gather_rows(const void* src, void* dst, const int64_t* index, int64_t row
  * out[b, t, h, :] (head_dim 128).  Replaces, at reference hilberta/flux_adapter.py:283-295,
  * attn.norm_q/norm_k/norm_added_q/norm_added_k (diffusers 0.36.0 RMSNorm), the torch.cat of text
  * and image tokens and apply_rotary_emb (use_real, interleaved pairs).  Tokens t < text_tokens
- * are read from src_text row t with weight_text, the others from src_image row t - text_tokens
- * with weight_image (element strides; rows hold heads*128 elements).  normalize=0 skips the
- * RMSNorm (weights must then be NULL); cos = sin = NULL skips the rotation; cos/sin are fp32
- * [tokens, 128] rows in output token order.  All pointers 16-byte aligned, strides multiples
- * of 8.  An in-place call (out aliasing a source) is not allowed. */
+ * are read from src_text row t, the others from src_image row t - text_tokens (element strides;
+ * rows hold heads*128 elements per plane).  planes = 2 prepares Q and K in one launch: plane p is
+ * read at column offset p * src_plane_stride and written at p * out_plane_stride.  weights is
+ * NULL or a host array of 2*planes device pointers {plane0 text, plane0 image, plane1 text,
+ * plane1 image} (entries may be NULL: no weight multiply).  normalize=0 skips the RMSNorm
+ * (weights must then be NULL); cos = sin = NULL skips the rotation; cos/sin are fp32
+ * [tokens, 128] rows in output token order.  All device pointers 16-byte aligned, strides
+ * multiples of 8.  The output must not overlap a source. */
 int hb_qk_prep(const void* src_text, const void* src_image, int64_t text_batch_stride,
                int64_t text_row_stride, int64_t image_batch_stride, int64_t image_row_stride,
-               int32_t batch, int32_t text_tokens, int32_t tokens, int32_t heads, int32_t head_dim,
-               int32_t dtype, int32_t normalize, const void* weight_text,
-               const void* weight_image, float eps, const float* cos, const float* sin, void* out,
-               int64_t out_batch_stride, int64_t out_row_stride, hb_stream_t stream);
+               int32_t planes, int64_t src_plane_stride, int32_t batch, int32_t text_tokens,
+               int32_t tokens, int32_t heads, int32_t head_dim, int32_t dtype, int32_t normalize,
+               const void* const* weights, float eps, const float* cos, const float* sin,
+               void* out, int64_t out_plane_stride, int64_t out_batch_stride,
+               int64_t out_row_stride, hb_stream_t stream);
+
+/* Gated residual update + AdaLN modulation, one pass per row (FLUX blocks).  For each of
+ * batch x rows rows of `hidden` values (row i of batch b at base + b*batch_stride + i*row_stride):
+ *   r = x + gate[b] * y            (skipped when y is NULL: r = x)
+ *   x_out = r                       (when x_out is not NULL; may be x itself)
+ *   out = shift[b] + LayerNorm(r) * (1 + scale[b])   (no affine, eps; fp32 statistics)
+ * with the 16-bit roundings of the torch sequence (r, the normalised row and 1 + scale are each
+ * rounded).  gate is [batch, hidden] with gate_batch_stride, shift/scale with mod_batch_stride.
+ * No counterpart in the
+ * reference's own code: it replaces diffusers 0.36.0 AdaLayerNormZero / AdaLayerNormZeroSingle /
+ * AdaLayerNormContinuous and the gated residual adds of FluxTransformerBlock and
+ * FluxSingleTransformerBlock, the blocks of the transformer hilberta/flux_adapter.py wraps.
+ * hidden is 512 * {1, 2, 3, 4, 6, 8}; pointers 16-byte aligned; strides multiples of 8;
+ * out must not overlap x or y. */
+int hb_adaln_modulate(int32_t batch, int32_t rows, int32_t hidden, int32_t dtype, float eps,
+                      const void* x, int64_t x_batch_stride, int64_t x_row_stride, const void* y,
+                      int64_t y_batch_stride, int64_t y_row_stride, const void* gate,
+                      int64_t gate_batch_stride, void* x_out,
+                      int64_t x_out_batch_stride, int64_t x_out_row_stride, const void* shift,
+                      const void* scale, int64_t mod_batch_stride, void* out,
+                      int64_t out_batch_stride, int64_t out_row_stride, hb_stream_t stream);
 
 /* ---------------------------------------------------------------- (b) block tables
  * Hilbert order of a grid_size x grid_size raster (reference hilberta/geometry.py:6-25). */

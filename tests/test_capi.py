@@ -38,10 +38,12 @@ def test_workspace_size_and_rejections():
 def test_qk_prep_rejections():
     lib = _lib.load()
     def call(head_dim=128, normalize=1, eps=1e-6, text_tokens=512, weight=None, stride=3072):
-        return lib.hb_qk_prep(None, None, 0, stride, 0, stride, 1, text_tokens, 4608, 24, head_dim,
-                              0, normalize, weight, None, eps, None, None, None, 0, 3072, None)
+        w = (ctypes.c_void_p * 2)(weight, None)
+        return lib.hb_qk_prep(None, None, 0, stride, 0, stride, 1, 0, 1, text_tokens, 4608, 24,
+                              head_dim, 0, normalize, w, eps, None, None, None, 0, 0, 3072, None)
 
     assert call(head_dim=64) == 1 and "head_dim" in _lib.last_error()
     assert call(text_tokens=5000) == 1 and "text_tokens" in _lib.last_error()
     assert call(normalize=1, eps=0.0) == 1
     assert call() == 1 and "null" in _lib.last_error()
+    assert call(normalize=0, weight=16) == 1

@@ -145,3 +145,29 @@ def test_argument_errors(hip_device):
         qk_prep(t, i, heads=2, normalize=False, weight_text=wt)
     with pytest.raises(ValueError):
         qk_prep(t.float(), i.float(), heads=2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_pair_launch_equals_two_single_launches(hip_device, dtype):
+    """planes=2 (Q and K from one fused projection in one launch) gives the same bits as two
+    single-plane launches, and matches the formulas within the tolerance above."""
+    from hilberta_amd.flux_inputs import qk_prep, qk_prep_pair
+
+    heads, T, grid = 24, 512, 64
+    W = heads * D
+    gen = torch.Generator("cpu").manual_seed(11)
+    N = T + grid * grid
+    qkv = torch.randn(2, N, 3 * W, generator=gen).to(dtype).to(hip_device)
+    w = [(torch.rand(D, generator=gen) + 0.5).to(dtype).to(hip_device) for _ in range(4)]
+    cos, sin = _tables(hip_device, T, grid, permute_seed=12)
+    say(f"case qk_prep_pair {dtype}")
+    qk = qk_prep_pair(qkv[:, :T, :2 * W], qkv[:, T:, :2 * W], heads=heads,
+                      weights=((w[0], w[1]), (w[2], w[3])), cos=cos, sin=sin)
+    q = qk_prep(qkv[:, :T, :W], qkv[:, T:, :W], heads=heads, weight_text=w[0], weight_image=w[1],
+                cos=cos, sin=sin)
+    k = qk_prep(qkv[:, :T, W:2 * W], qkv[:, T:, W:2 * W], heads=heads, weight_text=w[2],
+                weight_image=w[3], cos=cos, sin=sin)
+    torch.cuda.synchronize()
+    assert torch.equal(qk[0], q) and torch.equal(qk[1], k)
+    _check_normed(qk[1], qkv[:, :T, W:2 * W], qkv[:, T:, W:2 * W], heads, w[2], w[3], cos, sin,
+                  f"pair plane 1 {dtype}")
