@@ -370,11 +370,19 @@ class FluxTransformer:
 
     @torch.inference_mode()
     def forward(self, hidden_states, encoder_hidden_states, pooled_projections, timestep, img_ids,
-                txt_ids, guidance=None, *, attention=None):
-        """hidden_states [B, n, 64] packed latents (raster order), encoder_hidden_states
-        [B, T, 4096], pooled_projections [B, 768], timestep [B], img_ids [n, 3], txt_ids [T, 3]
-        -> predicted [B, n, 64] in raster order."""
+                txt_ids, guidance=None, *, attention=None, layout_scope="transformer"):
+        """hidden_states [B, n, 64] packed latents, encoder_hidden_states [B, T, 4096],
+        pooled_projections [B, 768], timestep [B], img_ids [n, 3], txt_ids [T, 3] -> predicted
+        [B, n, 64].
+
+        With a persistent layout, ``layout_scope="transformer"`` takes raster-order latents and
+        ids and returns a raster-order prediction (one gather at entry and exit of this call,
+        flux_adapter.py:209-212, :243); ``"sampling"`` takes latents and ids already in the plan's
+        order and returns the prediction in that order (the permutation lives at the sampling
+        loop's entry and exit instead, sampling_layout.py:88-116)."""
         s = self.shape
+        if layout_scope not in ("transformer", "sampling"):
+            raise ValueError("layout_scope must be transformer or sampling")
         attention = attention if attention is not None else NativeAttention()
         layout = attention.layout
         B, n, _ = hidden_states.shape
@@ -383,8 +391,9 @@ class FluxTransformer:
         if layout is not None:
             if N != layout.total_tokens:
                 raise ValueError("token count does not match the plan")
-            hidden_states = index_select_rows(hidden_states, 1, layout.order)
-            img_ids = index_select_rows(img_ids.contiguous(), 0, layout.order)
+            if layout_scope == "transformer":
+                hidden_states = index_select_rows(hidden_states, 1, layout.order)
+                img_ids = index_select_rows(img_ids.contiguous(), 0, layout.order)
         cos, sin = rotary_tables(torch.cat([txt_ids, img_ids]).to(self.device))
         double_mods, single_mods, out_mods = self._modulations(F.silu(self.temb(timestep, guidance,
                                                                                 pooled_projections)))
@@ -412,7 +421,7 @@ class FluxTransformer:
         if hn.shape[1] != n:   # no single blocks: the last double block modulated every row
             hn = hn[:, T:]
         out = F.linear(hn, *self.proj_out)
-        if layout is not None:
+        if layout is not None and layout_scope == "transformer":
             out = index_select_rows(out, 1, layout.inverse)
         return out
 
