@@ -182,6 +182,11 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
+  // The upper half of the persistent grid issues at a higher wave priority.  Two workgroups share
+  // each CU, and with equal priorities their waves tend to reach the MFMA and softmax phases
+  // together; the asymmetry lets one run ahead (5-7 % faster at 2048 px 16-tile K3, measured
+  // against the symmetric kernel in one process; neutral on dense tables).
+  if (blockIdx.x >= gridDim.x / 2) __builtin_amdgcn_s_setprio(1);
   // wave index as a provably uniform (scalar) value, so per-wave tests such as the flag check
   // compile to branches rather than exec-masked code
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
