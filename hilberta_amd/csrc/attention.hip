@@ -19,9 +19,9 @@
 //    query half may see are never loaded.
 //  * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16: each lane then
 //    holds 16 keys of ONE query, so the online-softmax row max is an in-lane max plus one
-//    cross-half exchange (ds_bpermute), and the output O^T = V^T P^T takes the score registers
-//    directly as the B operand; its A operand (V^T) comes out of LDS already transposed through
-//    ds_read_b64_tr_b16.
+//    cross-half exchange (v_permlane32_swap), and the output O^T = V^T P^T takes the score
+//    registers directly as the B operand; its A operand (V^T) comes out of LDS already
+//    transposed through ds_read_b64_tr_b16.
 //  * Each wave owns 32 queries; in paired mode waves 0-1 own query half 0 and waves 2-3 half 1.
 //    A block that the flag test (flags >> (half + 2*key_half)) & 1 of paired_kernel.py:65,83-84
 //    hides from a wave's half is computed but masked (P = 0), which keeps one code path.
@@ -102,15 +102,21 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   }
 }
 
-// x combined with the value held by the lane 32 positions away (ds_bpermute; `partner` is the
-// byte address ((lane ^ 32) << 2)).
-__device__ __forceinline__ float pair_max(float x, int partner) {
-  const float y = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(partner, __builtin_bit_cast(int, x)));
-  return fmaxf(x, y);
+// x combined with the value held by the lane 32 positions away: v_permlane32_swap exchanges the
+// two 32-lane halves of a register (no LDS round trip); of its two results, each lane holds its
+// own value in one and its partner's in the other.
+__device__ __forceinline__ float pair_max(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  // copied out first: this compiler lowers a bit cast of a vector element to element 0
+  const unsigned r0 = r[0], r1 = r[1];
+  return fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
 }
-__device__ __forceinline__ float pair_sum(float x, int partner) {
-  const float y = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(partner, __builtin_bit_cast(int, x)));
-  return x + y;
+__device__ __forceinline__ float pair_sum(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const unsigned r0 = r[0], r1 = r[1];
+  return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -193,7 +199,6 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   const int half = HALVES == 2 ? (wave * QW) / 64 : 0;
   const int ql = lane & 31;   // query (column) owned by this lane inside the wave's 32
   const int hl = lane >> 5;   // lane half: selects the 8-element k slice of MFMA operands
-  const int partner = (lane ^ 32) << 2;
 
   // ------------------------------------------------------------------ persistent work queues
   // Item codes: [0, total_g) are the chunks of global query tiles ((batch, head)-major, then tile,
@@ -416,7 +421,7 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   auto epilogue = [&]() {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      const float l_tot = pair_sum(l_run[g], partner);
+      const float l_tot = pair_sum(l_run[g]);
       const int q = cur.qfirst + wave * QW + g * 32 + ql;
       uint16_t* op = a.o + (int64_t)cur.b * a.o_sb + (int64_t)cur.h * a.o_sh + (int64_t)q * a.o_sn + hl * 4;
       float* lsep = a.lse ? a.lse + (int64_t)cur.bh * a.tokens + q : nullptr;
@@ -525,6 +530,18 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
       }
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4 * NG, 0);
       if (q_next) load_q(decode(nxt_idx));  // the current Q is dead after the score MFMAs
+      // the first two V operands, read before the softmax so their latency hides under it
+      const uint16_t* vt = stage + TILE;
+      constexpr int NPV = 4 * DT;
+      u32x4 vr[NPV];
+      auto vread = [&](int j) {  // operand of MFMA j: d-tile j % DT, key step j / DT
+        const int dt = j % DT, ks = j / DT;
+        const u32x2 lo = read_tr(vt + voff[dt][0] + ks * 16 * D);
+        const u32x2 hi = read_tr(vt + voff[dt][1] + ks * 16 * D);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      };
+#pragma unroll
+      for (int j = 0; j < 2; ++j) vr[j] = vread(j);
       // online softmax for query ql of each group (this lane holds 32 of its 64 keys)
       float mx[NG];
       bool resc = false;
@@ -537,7 +554,7 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
         for (int i = 0; i < 16; ++i) m = fmaxf(m, sc[g][1][i]);
         // A block this wave's query half may not see (paired flags) is computed but masked: its
         // row max counts as -inf (no rescale) and its exponent offset is -inf, so P = 0 exactly.
-        mx[g] = live ? pair_max(m, partner) * a.scale_log2 : -__builtin_inff();
+        mx[g] = live ? pair_max(m) * a.scale_log2 : -__builtin_inff();
         resc |= mx[g] > m_run[g] + RESCALE_LOG2;
       }
       // Lazy rescale: the exponent reference m_run moves only when some row's max exceeds it by
@@ -581,17 +598,6 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
         l_run[g] += l0 + l1;
       }
       // O^T += V^T P^T, V operands read two MFMAs ahead, each feeding NG MFMAs
-      const uint16_t* vt = stage + TILE;
-      constexpr int NPV = 4 * DT;
-      u32x4 vr[NPV];
-      auto vread = [&](int j) {  // operand of MFMA j: d-tile j % DT, key step j / DT
-        const int dt = j % DT, ks = j / DT;
-        const u32x2 lo = read_tr(vt + voff[dt][0] + ks * 16 * D);
-        const u32x2 hi = read_tr(vt + voff[dt][1] + ks * 16 * D);
-        return u32x4{lo[0], lo[1], hi[0], hi[1]};
-      };
-#pragma unroll
-      for (int j = 0; j < 2; ++j) vr[j] = vread(j);
 #pragma unroll
       for (int j = 0; j < NPV; ++j) {
         if (j + 2 < NPV) vr[j + 2] = vread(j + 2);
