@@ -183,6 +183,17 @@ def denoiser_bench(a):
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream(dev)
     grid = a.denoiser // 16
+    tuned = None
+    if a.tunableop:
+        # hipBLASLt / rocBLAS solution per GEMM shape, benchmarked once (during warmup) and written
+        # to the CSV when the process exits
+        tune = not os.path.exists(a.tunableop)
+        torch.cuda.tunable.enable(True)
+        torch.cuda.tunable.tuning_enable(tune)
+        torch.cuda.tunable.set_filename(a.tunableop)
+        if not tune:
+            torch.cuda.tunable.read_file(a.tunableop)
+        tuned = dict(file=os.path.basename(a.tunableop), tuned_here=tune)
     shape = FluxShape()
     log(f"denoiser {a.denoiser}px: building the random-init model ...")
     model = FluxTransformer(dev, shape, seed=0)
@@ -248,6 +259,7 @@ def denoiser_bench(a):
         "finite": finite,
         "parameters": model.parameter_count(),
         "kernels": kernels,
+        "tunableop": tuned,
         "timed_wall_ms": round(wall_ms, 1),
     }
     print(json.dumps(result), flush=True)
@@ -265,6 +277,9 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="attention only (for counter runs)")
     ap.add_argument("--denoiser", type=int, choices=(1024, 2048), default=0, metavar="PX",
                     help="time one FLUX-shaped denoiser step at PX (1024 or 2048) instead")
+    ap.add_argument("--tunableop", metavar="CSV", default=None,
+                    help="denoiser: select GEMM solutions with PyTorch TunableOp, reading CSV (tuning "
+                    "and writing it when it does not exist)")
     ap.add_argument("--modes", default="full,t4k1,t16k3",
                     help="denoiser attention modes to time (comma-separated subset of full,t4k1,t16k3)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
