@@ -67,6 +67,22 @@ def event_time(fn, reps, stream):
     return [s.elapsed_time(e) for s, e in times]
 
 
+def queued_time(fn, reps, stream, pad):
+    """Per-call ms of fn with the host's launch cost hidden: each rep first queues ``pad`` (about a
+    millisecond of unrelated GPU work), so the events and fn are all queued before the GPU reaches
+    them and the interval is GPU time only.  For kernels shorter than their host launch path."""
+    times = []
+    for _ in range(reps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        pad()
+        s.record(stream)
+        fn()
+        e.record(stream)
+        times.append((s, e))
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in times]
+
+
 def q10(xs, q):
     xs = sorted(xs)
     return xs[min(len(xs) - 1, int(q * len(xs)))]
@@ -265,6 +281,21 @@ def denoiser_bench(a):
     print(json.dumps(result), flush=True)
 
 
+def cpu_table_build_ms(tiles, k, grid):
+    """The oracle's numpy table build (bridge_k_plan + pair_metadata, four phases) on the host."""
+    root = os.path.dirname(os.path.abspath(__file__))
+    if root not in sys.path:
+        sys.path.insert(0, root)
+    from oracle import topology as T
+
+    t0 = time.perf_counter()
+    plan = T.bridge_k_plan(tiles, k, False, grid_size=grid)
+    for p in plan["phases"]:
+        T.pair_metadata(p["kv_indices"], p["kv_counts"], tokens=plan["total_tokens"],
+                        global_tokens=plan["global_tokens"])
+    return round((time.perf_counter() - t0) * 1e3, 1)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -275,6 +306,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="attention only (for counter runs)")
+    ap.add_argument("--full-tables", action="store_true",
+                    help="time the kernel on all-connection tables instead (dense comparison for "
+                    "counter runs: skipped blocks never touch HBM)")
     ap.add_argument("--denoiser", type=int, choices=(1024, 2048), default=0, metavar="PX",
                     help="time one FLUX-shaped denoiser step at PX (1024 or 2048) instead")
     ap.add_argument("--tunableop", metavar="CSV", default=None,
@@ -324,6 +358,18 @@ def main():
     N, G = plan.total_tokens, plan.global_tokens
     T = N // 64
     metas = plan.phases
+    # algorithmic bytes of the table build: per phase the nb x nb int32 bridge-score matrix and the
+    # emitted paired tables (ids, flags, counts)
+    nb = (N - 512) // 64
+    table_bytes = sum(nb * nb * 4 + (m.kv_indices.numel() + m.kv_flags.numel() + m.kv_counts.numel()) * 4
+                      for m in metas)
+    if a.full_tables:
+        from hilberta_amd.paired_metadata import PairedMetadata
+
+        ids = torch.arange(T, dtype=torch.int32, device=dev).repeat((N - G) // 128, 1).contiguous()
+        full = PairedMetadata(ids, torch.full_like(ids, 3),
+                              torch.full(((N - G) // 128,), T, dtype=torch.int32, device=dev), N, G, 64)
+        metas = [full] * 4
     live = [live_blocks(m) for m in metas]
 
     gen = torch.Generator("cpu").manual_seed(2707)
@@ -391,17 +437,32 @@ def main():
             lat = torch.randn(a.batch, n_img, 64, device=dev).to(torch.bfloat16)
             hid = torch.randn(a.batch, n_img, 3072, device=dev).to(torch.bfloat16)
             order = plan.layout.image_order
+            # stream bandwidth: a plain 1 GiB device-to-device copy (read + write); the same copy
+            # is the padding that hides host launch cost in the per-size timings below
+            src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+            dst = torch.empty_like(src)
+            pad = lambda: dst.copy_(src)  # noqa: E731
+            for _ in range(2):
+                pad()
+            copy_ms = statistics.median(event_time(pad, 10, stream))
             perm = {}
             for name, x in (("latents_64", lat), ("hidden_3072", hid)):
-                fn = lambda x=x: index_select_rows(x, 1, order)  # noqa: E731
+                y = torch.empty_like(x)
+                fn = lambda x=x, y=y: index_select_rows(x, 1, order, out=y)  # noqa: E731
                 for _ in range(3):
                     fn()
-                t = statistics.median(event_time(fn, 20, stream))
+                t = statistics.median(queued_time(fn, 20, stream, pad))
                 nbytes = 2 * x.numel() * x.element_size() + order.numel() * 8
-                ref = statistics.median(event_time(lambda x=x: x.index_select(1, order), 20, stream))
+                ref = statistics.median(queued_time(lambda x=x: x.index_select(1, order), 20, stream, pad))
+                cp = statistics.median(queued_time(lambda x=x, y=y: y.copy_(x), 20, stream, pad))
                 perm[name] = dict(us=round(t * 1e3, 2), GBps=round(nbytes / (t * 1e-3) / 1e9, 1),
-                                  torch_index_select_us=round(ref * 1e3, 2))
+                                  torch_index_select_us=round(ref * 1e3, 2),
+                                  same_size_copy_us=round(cp * 1e3, 2),
+                                  same_size_copy_GBps=round(2 * x.numel() * x.element_size()
+                                                            / (cp * 1e-3) / 1e9, 1))
+            del src, dst, pad
             extras = dict(
+                stream_copy_GBps=round(2 * (1 << 30) / (copy_ms * 1e-3) / 1e9, 1),
                 dense_sdpa_ms=round(dense_sdpa, 4),
                 dense_sdpa_tflops=round(dense_flops / (dense_sdpa * 1e-3) / 1e12, 1),
                 dense_own_kernel_ms=round(dense_own, 4),
@@ -427,7 +488,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic: bf16 Q/K/V ~ N(0,1) from CPU seed 2707, resident in HBM",
         "config": {
-            "workload": f"FLUX {a.config}: paired block-sparse attention fwd, "
+            "workload": f"FLUX {a.config}{' (all-connection tables)' if a.full_tables else ''}: "
+            "paired block-sparse attention fwd, "
             f"B={a.batch} H={HEADS} D={DIM} N={N} (512 text + {N - 512} image), 4 phases/step",
             "global_batch": a.batch,
             "seq_len": N,
@@ -442,6 +504,8 @@ def main():
         "phase_live_tflops": [round(x, 1) for x in tflops],
         "mfma_util": round(achieved / PEAK_BF16_TFLOPS, 4),
         "table_build_ms": round(table_ms, 3),
+        "table_build_bytes": table_bytes,
+        "table_build_GBps": round(table_bytes / (table_ms * 1e-3) / 1e9, 2),
         "timed_wall_ms": round(wall_ms, 2),
         "roofline": {
             "bound": "mfma",
@@ -458,6 +522,7 @@ def main():
     if not a.no_cpu_baseline:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(q, k_, v, metas[0], a.cpu_budget)
+        result["cpu_baseline"]["table_build_ms"] = cpu_table_build_ms(tiles, k, grid)
     print(json.dumps(result), flush=True)
 
 

@@ -135,6 +135,22 @@ def test_paired_2048_batch2_bnhd_key_block_128(hip_device):
     _sampled_rows_check(out, lse, qd, kd, vd, plan, 3, rows, "2048 B=2 KB128")
 
 
+@pytest.mark.parametrize("shape", [(1, 100_000_000, 3), (1500, 1_000_000, 3)])
+def test_permutation_byte_rows_long_walks(hip_device, shape):
+    """3-byte rows move one byte per thread: 3e8 bytes take the grid-stride loop of the 32-bit
+    walk, 4.5e9 bytes the 64-bit walk; both bit-exact against torch's index_select."""
+    from hilberta_amd.layout import index_select_rows
+
+    gen = torch.Generator(hip_device).manual_seed(13)
+    x = torch.randint(0, 256, shape, dtype=torch.uint8, device=hip_device, generator=gen)
+    index = torch.randperm(shape[1], device=hip_device, generator=gen)
+    say(f"case byte-row permutation {shape}")
+    out = index_select_rows(x, 1, index)
+    assert torch.equal(out, x.index_select(1, index))
+    del out
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("shape,dim", [((1, 65536, 64), 1), ((1, 66048, 24, 128), 1)])
 def test_permutation_4096_sizes(hip_device, shape, dim):
     """4096 px latents and BNHD projections: gather and its inverse are bit-exact."""
