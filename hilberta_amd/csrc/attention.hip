@@ -24,7 +24,9 @@
 //    transposed through ds_read_b64_tr_b16.
 //  * Each wave owns 32 queries; in paired mode waves 0-1 own query half 0 and waves 2-3 half 1.
 //    A block that the flag test (flags >> (half + 2*key_half)) & 1 of paired_kernel.py:65,83-84
-//    hides from a wave's half is computed but masked (P = 0), which keeps one code path.
+//    hides from a wave's half is computed but masked (P = 0), which keeps one code path (a
+//    wave-uniform branch around the masked case measured slower: the compiler's schedule of the
+//    common path degrades).
 //  * Online softmax in exp2 with fp32 state (paired_kernel.py:82-93) and a lazy rescale; P is
 //    rounded to the input type before the PV product as in the reference; an optional fp32
 //    per-row logsumexp (natural log) is written as well.
@@ -39,12 +41,10 @@ constexpr float LN2 = 0.69314718055994530942f;
 constexpr int QUEUES = 8;    // one work queue per XCD
 constexpr float RESCALE_LOG2 = 8.0f;  // lazy-rescale threshold (log2 units)
 constexpr int MAX_SPLIT = 16;  // chunks per global query tile, at most
-#ifndef HB_SPLIT_DIV
-#define HB_SPLIT_DIV 1
-#endif
-constexpr int SPLIT_DIV = HB_SPLIT_DIV;
-constexpr int NOMINAL_GROUPS = 512;
- // persistent workgroups on a full MI355X (2 per CU)
+constexpr int NOMINAL_GROUPS = 512;  // persistent workgroups on a full MI355X (2 per CU)
+// V operands (ds_read_b64_tr_b16 pairs) in flight ahead of the PV MFMAs: three cover the LDS
+// latency under load better than two (2-3 % at 2048 px 16-tile K3, bitwise-identical results)
+constexpr int PFV = 3;
 // word 3 of a raw buffer resource (32-bit data format, no swizzle), as for gfx9-family buffers
 constexpr int BUFFER_WORD3 = 0x00020000;
 // __builtin_amdgcn_sched_group_barrier instruction classes
@@ -530,7 +530,7 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
       }
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4 * NG, 0);
       if (q_next) load_q(decode(nxt_idx));  // the current Q is dead after the score MFMAs
-      // the first two V operands, read before the softmax so their latency hides under it
+      // the first PFV V operands, read before the softmax so their latency hides under it
       const uint16_t* vt = stage + TILE;
       constexpr int NPV = 4 * DT;
       u32x4 vr[NPV];
@@ -541,7 +541,7 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
         return u32x4{lo[0], lo[1], hi[0], hi[1]};
       };
 #pragma unroll
-      for (int j = 0; j < 2; ++j) vr[j] = vread(j);
+      for (int j = 0; j < PFV; ++j) vr[j] = vread(j);
       // online softmax for query ql of each group (this lane holds 32 of its 64 keys)
       float mx[NG];
       bool resc = false;
@@ -597,20 +597,19 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
         }
         l_run[g] += l0 + l1;
       }
-      // O^T += V^T P^T, V operands read two MFMAs ahead, each feeding NG MFMAs
+      // O^T += V^T P^T, V operands read PFV MFMAs ahead, each feeding NG MFMAs
 #pragma unroll
       for (int j = 0; j < NPV; ++j) {
-        if (j + 2 < NPV) vr[j + 2] = vread(j + 2);
+        if (j + PFV < NPV) vr[j + PFV] = vread(j + PFV);
 #pragma unroll
         for (int g = 0; g < NG; ++g) acc[g][j % DT] = mfma32<F16>(vr[j], pk[g][j / DT], acc[g][j % DT]);
       }
-      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 4, 1);
 #pragma unroll
-      for (int j = 0; j < NPV - 2; ++j) {
+      for (int j = 0; j < NPV - PFV; ++j) {
         __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 1);
         __builtin_amdgcn_sched_group_barrier(SG_MFMA, NG, 1);
       }
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2 * NG, 1);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, PFV * NG, 1);
     }
     if (!cross) {
       s = sn;
@@ -737,7 +736,7 @@ int make_plan(Plan& p, int batch, int heads, int tokens, int head_dim, int globa
   const int64_t row_steps = (int64_t)width * p.kbr;
   const int64_t all_steps =
       (int64_t)batch * heads * ((int64_t)p.rows * row_steps + (int64_t)p.global_tiles * p.key_blocks);
-  int64_t target = (all_steps + NOMINAL_GROUPS - 1) / NOMINAL_GROUPS / SPLIT_DIV;
+  int64_t target = (all_steps + NOMINAL_GROUPS - 1) / NOMINAL_GROUPS;
   if (target < row_steps) target = row_steps;
   int nsplit = (int)((p.key_blocks + target - 1) / target);
   nsplit = nsplit < 1 ? 1 : (nsplit > MAX_SPLIT ? MAX_SPLIT : nsplit);
