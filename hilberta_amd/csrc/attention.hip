@@ -321,7 +321,11 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     kb = __builtin_amdgcn_readlane(t_id, e - tbase) * KBR + sub;
     fl = HALVES == 2 ? (__builtin_amdgcn_readlane(t_fl, e - tbase) >> (2 * sub)) & 3 : 1;
   };
+  // First step at or after s that some query half may see.  With one step per table entry every
+  // entry qualifies (paired entries carry at least one flag bit), so only 128-key blocks (two
+  // steps per entry, one of which may be hidden from both halves) need the search.
   auto next_live = [&](int s) {
+    if (KBR == 1) return s;
     for (; s < cur.nsteps; ++s) {
       int kb, fl;
       step_info(s, kb, fl);
@@ -458,20 +462,18 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   // loaded right after the last score MFMAs of the current item.
   const uint16_t* cur_k = k_base(cur);
   const uint16_t* cur_v = v_base(cur);
+  // block and flags of the current step, computed while the step before it issued their loads
+  int c_kb = 0, c_fl = 0;
   if (cur.valid) {
   load_q(cur);
-  {
-    int kb, fl;
-    step_info(0, kb, fl);
-    dma_block(lds0, cur_k, cur_v, kb);
-  }
+  step_info(0, c_kb, c_fl);
+  dma_block(lds0, cur_k, cur_v, c_kb);
   int s = 0;
   // One step on `stage` while the next block streams into `other`.  The two stages are distinct
   // LDS arrays and the loop below alternates them at compile time, so the compiler can see that
   // reads of `stage` never alias the loads in flight into `other`.  Returns true when done.
   auto step = [&](uint16_t* __restrict__ stage, uint16_t* __restrict__ other) -> bool {
-    int kb, fl;
-    step_info(s, kb, fl);
+    const int fl = c_fl;
     if (claiming && tid == 0) s_claim[0] = claim_from(pending);
     // every wave's loads of this stage have landed (each wave waits for its own, then the
     // barrier), and every wave is done reading the other stage, which the next block's loads may
@@ -486,13 +488,14 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     const int sn = next_live(s + 1);
     const bool cross = sn >= cur.nsteps;
     if (!cross) {
-      int kbn, fln;
-      step_info(sn, kbn, fln);
-      dma_block(other, cur_k, cur_v, kbn);
+      step_info(sn, c_kb, c_fl);
+      dma_block(other, cur_k, cur_v, c_kb);
     } else if (nxt_idx >= 0) {
+      // step 0 of the next item: its first key block is global, seen by both query halves
       const Item nxt = decode(nxt_idx);
-      const int kbn = nxt.global ? nxt.first_block : __builtin_amdgcn_readlane(n_id, 0) * KBR;
-      dma_block(other, k_base(nxt), v_base(nxt), kbn);
+      c_kb = nxt.global ? nxt.first_block : __builtin_amdgcn_readlane(n_id, 0) * KBR;
+      c_fl = 3;
+      dma_block(other, k_base(nxt), v_base(nxt), c_kb);
     }
     const bool live = (fl >> half) & 1;
     const bool q_next = cross && nxt_idx >= 0;
