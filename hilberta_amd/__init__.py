@@ -8,6 +8,11 @@ rebuilt on hand-written HIP kernels behind a C ABI (include/hilberta_hip.h):
                     block tables built on the GPU, bit-exact with the reference
   paired_kernel / sparse_kernel
                     block-sparse flash-attention forward (bf16/fp16 MFMA, persistent)
+  flux_inputs / flux_norm
+                    FLUX attention inputs (RMSNorm + rotary + [text; image] layout) and the
+                    gated-residual AdaLN pass, one HIP kernel each
+  flux_model / sampling_layout
+                    a FLUX-shaped denoiser step on these kernels and the sampling-scope layout
 
 The modules keep the reference package's call surface.  There is no CPU fallback: the HIP library
 (python -m hilberta_amd.build) and a GPU are required for every computation.
