@@ -46,6 +46,10 @@ CONFIGS = {
 }
 HEADS, DIM = 24, 128
 WEIGHTS = (15, 14, 14, 14)
+KERNEL_NAMES = {"paired": "attn_fwd_kernel<2,128,1,false> (hb_paired_fwd)",
+                "paired128": "attn_fwd_kernel<2,128,2,false> (hb_paired_fwd)",
+                "unpaired": "attn_fwd_kernel<1,128,1,false> (hb_block_sparse_fwd)"}
+TABLE_NAMES = {"paired": "paired", "paired128": "paired KV128", "unpaired": "unpaired (sparse_attention)"}
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 
@@ -306,6 +310,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="attention only (for counter runs)")
+    ap.add_argument("--tables", choices=("paired", "paired128", "unpaired"), default="paired",
+                    help="table format timed: paired 64-key blocks (the reference's default), paired "
+                    "128-key blocks, or the unpaired sparse_attention entry")
     ap.add_argument("--full-tables", action="store_true",
                     help="time the kernel on all-connection tables instead (dense comparison for "
                     "counter runs: skipped blocks never touch HBM)")
@@ -363,14 +370,27 @@ def main():
     nb = (N - 512) // 64
     table_bytes = sum(nb * nb * 4 + (m.kv_indices.numel() + m.kv_flags.numel() + m.kv_counts.numel()) * 4
                       for m in metas)
+    unpaired = None
+    if a.tables == "paired128":
+        metas = paired_plan_device(tiles, k, grid_size=grid, key_block_size=128, device=dev).phases
+    elif a.tables == "unpaired":
+        from hilberta_amd.bridge_k import bridge_k_plan
+
+        host = bridge_k_plan(tiles, k, False, grid_size=grid)
+        unpaired = [(ph.kv_indices.to(dev), ph.kv_counts.to(dev)) for ph in host.phases]
     if a.full_tables:
+        if a.tables != "paired":
+            ap.error("--full-tables times the paired 64-key format only")
         from hilberta_amd.paired_metadata import PairedMetadata
 
         ids = torch.arange(T, dtype=torch.int32, device=dev).repeat((N - G) // 128, 1).contiguous()
         full = PairedMetadata(ids, torch.full_like(ids, 3),
                               torch.full(((N - G) // 128,), T, dtype=torch.int32, device=dev), N, G, 64)
         metas = [full] * 4
-    live = [live_blocks(m) for m in metas]
+    if unpaired is None:
+        live = [live_blocks(m) for m in metas]
+    else:
+        live = [(G // 64) * T + int(c.sum()) for _, c in unpaired]
 
     gen = torch.Generator("cpu").manual_seed(2707)
     shape = (a.batch, HEADS, N, DIM)
@@ -379,8 +399,14 @@ def main():
     out = torch.empty_like(q)
 
     with torch.inference_mode():
-        calls = [lambda m=m: paired_attention(q, k_, v, m, global_strategy="triton", num_warps=8,
-                                              out=out) for m in metas]
+        if unpaired is None:
+            calls = [lambda m=m: paired_attention(q, k_, v, m, global_strategy="triton", num_warps=8,
+                                                  out=out) for m in metas]
+        else:
+            from hilberta_amd.sparse_kernel import sparse_attention
+
+            calls = [lambda t=t: sparse_attention(q, k_, v, t[0], t[1], global_tokens=G,
+                                                  global_strategy="triton", out=out) for t in unpaired]
         for _ in range(a.warmup):
             for fn in calls:
                 fn()
@@ -446,14 +472,16 @@ def main():
                 pad()
             copy_ms = statistics.median(event_time(pad, 10, stream))
             perm = {}
-            for name, x in (("latents_64", lat), ("hidden_3072", hid)):
+            ids = torch.randn(n_img, 3, device=dev)
+            for name, x, dim in (("latents_64", lat, 1), ("hidden_3072", hid, 1), ("ids_3", ids, 0)):
                 y = torch.empty_like(x)
-                fn = lambda x=x, y=y: index_select_rows(x, 1, order, out=y)  # noqa: E731
+                fn = lambda x=x, y=y, dim=dim: index_select_rows(x, dim, order, out=y)  # noqa: E731
                 for _ in range(3):
                     fn()
                 t = statistics.median(queued_time(fn, 20, stream, pad))
                 nbytes = 2 * x.numel() * x.element_size() + order.numel() * 8
-                ref = statistics.median(queued_time(lambda x=x: x.index_select(1, order), 20, stream, pad))
+                ref = statistics.median(queued_time(lambda x=x, dim=dim: x.index_select(dim, order), 20,
+                                                    stream, pad))
                 cp = statistics.median(queued_time(lambda x=x, y=y: y.copy_(x), 20, stream, pad))
                 perm[name] = dict(us=round(t * 1e3, 2), GBps=round(nbytes / (t * 1e-3) / 1e9, 1),
                                   torch_index_select_us=round(ref * 1e3, 2),
@@ -471,9 +499,15 @@ def main():
                 speedup_vs_dense_own=round(dense_own / weighted, 3),
                 speedup_target=round(0.8 / density, 3),
                 permute=perm,
+                # one attention call plus its share of one forward's layout moves (latents in and
+                # out, image ids in) over the 57 attention layers, as the reference's csv reports it
+                attention_plus_amortised_layout_ms=round(
+                    weighted + (2 * perm["latents_64"]["us"] + perm["ids_3"]["us"]) / 57 / 1e3, 4),
             )
 
-    traffic, traffic_src = profiled_traffic(a.config)
+    # the committed counter summaries cover the paired 64-key format on the configs' own tables
+    traffic, traffic_src = (profiled_traffic(a.config) if a.tables == "paired" and not a.full_tables
+                            else (None, None))
     result = {
         "metric": "sparse-attn fwd ms + live-block MFMA util, FLUX 2048px 16-tile K3 vs dense",
         "value": round(weighted, 4),
@@ -489,7 +523,7 @@ def main():
         "data": "synthetic: bf16 Q/K/V ~ N(0,1) from CPU seed 2707, resident in HBM",
         "config": {
             "workload": f"FLUX {a.config}{' (all-connection tables)' if a.full_tables else ''}: "
-            "paired block-sparse attention fwd, "
+            f"{TABLE_NAMES[a.tables]} block-sparse attention fwd, "
             f"B={a.batch} H={HEADS} D={DIM} N={N} (512 text + {N - 512} image), 4 phases/step",
             "global_batch": a.batch,
             "seq_len": N,
@@ -509,7 +543,7 @@ def main():
         "timed_wall_ms": round(wall_ms, 2),
         "roofline": {
             "bound": "mfma",
-            "kernel": "attn_fwd_kernel<2,128,1,false> (hb_paired_fwd)",
+            "kernel": KERNEL_NAMES[a.tables],
             "achieved": round(achieved, 1),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
