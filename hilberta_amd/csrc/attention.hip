@@ -375,9 +375,14 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   const int vround_bytes = ROWS_PER_ROUND * (int)a.v_sn * 2;
   auto dma_block = [&](uint16_t* stage, const uint16_t* kbase, const uint16_t* vbase, int kb) {
     const int sk = kb * kblk_bytes, sv = kb * vblk_bytes;
+    // The wave index enters the LDS destinations through an opaque copy, so each launch rebuilds
+    // them with scalar adds; left visible, the compiler hoists all 16 destinations of both stages
+    // out of the loop and, short of scalar registers, reloads them from VGPR lanes every step.
+    int w = wave;
+    asm volatile("" : "+s"(w));
 #pragma unroll
     for (int n = 0; n < NDMA; ++n) {
-      const int i = n * WAVES + wave;
+      const int i = n * WAVES + w;
       if (CPR % WAVES == 0 || i < CPR) {
         const int o = DMA_LINEAR ? 0 : n;
         const int rk = DMA_LINEAR ? n * kround_bytes : 0, rv = DMA_LINEAR ? n * vround_bytes : 0;
