@@ -112,8 +112,14 @@ def phase_bits_device(layout: DeviceLayout, tile_count, phase, bridge_mode, k, s
     return bits, chosen
 
 
-def emit_device(bits, total_blocks, *, unpaired=True, paired=False, key_block_size=64):
-    """Tables from a bitmap: returns dict with ids/counts and/or paired ids/flags/counts (device)."""
+def emit_device(bits, total_blocks, *, unpaired=True, paired=False, key_block_size=64,
+                paired_width=None):
+    """Tables from a bitmap: returns dict with ids/counts and/or paired ids/flags/counts (device).
+
+    The table widths are the widest rows, read back to the host (one synchronisation), unless only
+    paired tables are asked for with ``paired_width`` given: an upper bound on the paired row
+    length, used as is (rows zero-padded to it), with no host synchronisation.
+    """
     device = bits.device
     lib = _lib.load()
     rows = bits.shape[0]
@@ -126,7 +132,10 @@ def emit_device(bits, total_blocks, *, unpaired=True, paired=False, key_block_si
                             counts.data_ptr() if unpaired else None,
                             pcounts.data_ptr() if paired else None, maxc.data_ptr(), stream)
     _lib.check(rc, "hb_bits_counts")
-    width, pwidth = (max(x, 1) for x in maxc.tolist())  # setup-time sync: table widths
+    if paired_width is not None and not unpaired:
+        width, pwidth = 1, int(paired_width)
+    else:
+        width, pwidth = (max(x, 1) for x in maxc.tolist())  # setup-time sync: table widths
     ids = torch.empty((rows, width), **i32) if unpaired else None
     pids = torch.empty((rows // 2, pwidth), **i32) if paired else None
     pflags = torch.empty((rows // 2, pwidth), **i32) if paired else None

@@ -181,9 +181,22 @@ def _strides(q, k, v, out):
 
 def _block_sparse_fwd(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, scale_log2,
                       all_queries):
-    """Launch hb_block_sparse_fwd on the current stream (module-level so tests can patch it)."""
-    lib = _lib.load()
+    """Launch the unpaired tables on the current stream (module-level so tests can patch it).
+
+    When the 64-query rows pair up (N and the global prefix multiples of 128), consecutive rows
+    2r, 2r + 1 are merged on the device, as pair_metadata does (paired_metadata.py:26-51), and run
+    on hb_paired_fwd: a 128-query item then keeps two waves per SIMD busy where a 64-query item
+    keeps one.  Every query sees the same key blocks in the same ascending order with the same
+    arithmetic; blocks of the other half are masked to exact zeros.  The merge runs three small
+    kernels into tables padded to min(2 * width, N / 64) entries, with no host synchronisation.
+    Otherwise the rows run as they are on hb_block_sparse_fwd.
+    """
     B, H, N, D = q.shape
+    if N % 128 == 0 and global_tokens % 128 == 0:
+        _paired_from_unpaired(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, scale_log2,
+                              all_queries)
+        return
+    lib = _lib.load()
     width = kv_indices.shape[1]
     ws = attention_workspace(q.device, B, H, N, D, global_tokens, width, 64, paired=0,
                              all_queries=all_queries)
@@ -196,6 +209,31 @@ def _block_sparse_fwd(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, s
         _lib.stream_ptr(q.device),
     )
     _lib.check(rc, "hb_block_sparse_fwd")
+
+
+def _paired_from_unpaired(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, scale_log2,
+                          all_queries):
+    """Pair 64-query tables on the device and launch hb_paired_fwd (see _block_sparse_fwd)."""
+    from ._tables import emit_device, table_bits_device
+
+    lib = _lib.load()
+    B, H, N, D = q.shape
+    blocks = N // 64
+    bits = table_bits_device(kv_indices, kv_counts, blocks)
+    width = min(2 * kv_indices.shape[1], blocks)
+    t = emit_device(bits, blocks, unpaired=False, paired=True, key_block_size=64, paired_width=width)
+    ids, flags, counts = t["paired_indices"], t["paired_flags"], t["paired_counts"]
+    ws = attention_workspace(q.device, B, H, N, D, global_tokens, width, 64, paired=1,
+                             all_queries=all_queries)
+    strides = (ctypes.c_int64 * 12)(*_strides(q, k, v, out))
+    rc = lib.hb_paired_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+        lse.data_ptr() if lse is not None else None, strides, B, H, N, D,
+        1 if q.dtype == torch.float16 else 0, ids.data_ptr(), flags.data_ptr(), counts.data_ptr(),
+        width, global_tokens, 64, int(all_queries), scale_log2, ws.data_ptr(), ws.numel(), 0,
+        _lib.stream_ptr(q.device),
+    )
+    _lib.check(rc, "hb_paired_fwd")
 
 
 def sparse_attention(

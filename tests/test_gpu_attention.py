@@ -101,6 +101,86 @@ def test_unpaired_sparse_attention(hip_device):
         compare(out.cpu(), lse.cpu(), ref_o, ref_l, f"unpaired phase {phase}")
 
 
+def _unpaired_kernel(q, k, v, ids, counts, global_tokens, scale):
+    """The 64-query-row kernel itself (hb_block_sparse_fwd through the C ABI), output and LSE."""
+    import ctypes
+    import math as m
+
+    from hilberta_amd import _lib
+    from hilberta_amd._workspace import attention_workspace
+    from hilberta_amd.sparse_kernel import _strides
+
+    lib = _lib.load()
+    B, H, N, Dh = q.shape
+    out = torch.empty_like(q)
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
+    width = ids.shape[1]
+    ws = attention_workspace(q.device, B, H, N, Dh, global_tokens, width, 64, paired=0, all_queries=1)
+    strides = (ctypes.c_int64 * 12)(*_strides(q, k, v, out))
+    rc = lib.hb_block_sparse_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                 strides, B, H, N, Dh, 0, ids.data_ptr(), counts.data_ptr(), width,
+                                 global_tokens, 64, 1, scale * 1.4426950408889634, ws.data_ptr(),
+                                 ws.numel(), 0, _lib.stream_ptr(q.device))
+    _lib.check(rc, "hb_block_sparse_fwd")
+    return out, lse
+
+
+def test_unpaired_tables_run_paired(hip_device):
+    """sparse_attention pairs 64-query rows on the device and runs the paired kernel: every
+    ordinary query row equals the unpaired kernel's bit for bit (same blocks, same order, same
+    arithmetic; the other half's blocks add exact zeros); the global rows, chunked differently,
+    agree within the suite's tolerance."""
+    from hilberta_amd.sparse_kernel import sparse_attention
+
+    plan = oracle_plan("1024_t16k3")
+    G = plan["global_tokens"]
+    q, k, v = _qkv(plan, heads=4, seed=21)
+    qd, kd, vd = (x.to(hip_device) for x in (q, k, v))
+    for phase in (1, 2):
+        say(f"case unpaired tables via the paired kernel, 1024_t16k3 phase {phase}")
+        p = plan["phases"][phase]
+        ids = torch.from_numpy(p["kv_indices"]).to(hip_device)
+        counts = torch.from_numpy(p["kv_counts"]).to(hip_device)
+        lse = torch.empty(q.shape[:3], dtype=torch.float32, device=hip_device)
+        out = sparse_attention(qd, kd, vd, ids, counts, global_tokens=G, lse=lse)
+        ref_o, ref_l = _unpaired_kernel(qd, kd, vd, ids, counts, G, D ** -0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(out[:, :, G:], ref_o[:, :, G:]), "ordinary rows differ"
+        assert torch.equal(lse[:, :, G:], ref_l[:, :, G:]), "ordinary LSE differs"
+        # the global rows are split into chunks differently, so P is rounded to bf16 against
+        # different running maxima: equal to the suite's tolerance, not bit for bit
+        assert (out[:, :, :G].float() - ref_o[:, :, :G].float()).abs().max().item() <= 4e-3
+        assert (lse[:, :, :G] - ref_l[:, :, :G]).abs().max().item() <= 1e-3
+
+
+def test_unpaired_odd_rows_use_unpaired_kernel(hip_device):
+    """Tables whose 64-query rows do not pair (an odd number of them) run on the 64-query-row
+    kernel; against the fp32 oracle on random valid tables."""
+    from hilberta_amd.sparse_kernel import sparse_attention
+
+    G, rows = 512, 9
+    N = G + 64 * rows
+    T_ = N // 64
+    rng = np.random.default_rng(5)
+    width = G // 64 + 6
+    ids = np.zeros((rows, width), np.int32)
+    counts = np.zeros(rows, np.int32)
+    for r in range(rows):
+        extra = rng.choice(np.arange(G // 64, T_), size=rng.integers(1, 7), replace=False)
+        row = np.concatenate([np.arange(G // 64), np.sort(extra)]).astype(np.int32)
+        ids[r, :len(row)] = row
+        counts[r] = len(row)
+    q, k, v = A.seeded_qkv(1, 3, N, D, seed=8)
+    qd, kd, vd = (x.to(hip_device) for x in (q, k, v))
+    say(f"case unpaired odd rows N={N}")
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=hip_device)
+    out = sparse_attention(qd, kd, vd, torch.from_numpy(ids).to(hip_device),
+                           torch.from_numpy(counts).to(hip_device), global_tokens=G, lse=lse)
+    torch.cuda.synchronize()
+    ref_o, ref_l = A.block_sparse_attention(q, k, v, ids, counts, global_tokens=G)
+    compare(out.cpu(), lse.cpu(), ref_o, ref_l, "unpaired odd rows")
+
+
 @pytest.mark.parametrize("dtype,dim", [(torch.float16, 128), (torch.bfloat16, 64), (torch.float16, 64)])
 def test_dtypes_and_head_dim(hip_device, dtype, dim):
     from hilberta_amd.paired_kernel import paired_attention
