@@ -5,9 +5,10 @@
 //
 //  * Work item = one query tile (128 queries for paired tables, 64 for unpaired ones) of one
 //    (batch, head), or one chunk of a global (text) query tile's all-key sweep.  Global tiles are
-//    split into at most MAX_SPLIT chunks, none shorter than the longest ordinary row, so no item
-//    dominates the schedule; chunk partials (unnormalised accumulator, running max, row sum) go to
-//    the workspace and merge_kernel combines them after the main kernel.
+//    split into at most MAX_SPLIT chunks of about half a workgroup's average work, none shorter
+//    than the longest ordinary row or MIN_CHUNK steps, so no item dominates the schedule; chunk
+//    partials (unnormalised accumulator, running max, row sum) go to the workspace and
+//    merge_kernel combines them after the main kernel.
 //  * Persistent workgroups (2 per CU) claim items from 8 work queues, one per XCD (queue x =
 //    blockIdx % 8, the XCD under round-robin dispatch, owns a contiguous range of the item list),
 //    so items that share K/V blocks run under one L2; idle workgroups steal from other queues.
@@ -42,6 +43,7 @@ constexpr int QUEUES = 8;    // one work queue per XCD
 constexpr float RESCALE_LOG2 = 8.0f;  // lazy-rescale threshold (log2 units)
 constexpr int MAX_SPLIT = 16;  // chunks per global query tile, at most
 constexpr int NOMINAL_GROUPS = 512;  // persistent workgroups on a full MI355X (2 per CU)
+constexpr int MIN_CHUNK = 64;  // key-block steps per global chunk, at least (shorter chunks' fixed costs show)
 // V operands (ds_read_b64_tr_b16 pairs) in flight ahead of the PV MFMAs: three cover the LDS
 // latency under load better than two (2-3 % at 2048 px 16-tile K3, bitwise-identical results)
 constexpr int PFV = 3;
@@ -738,14 +740,18 @@ int make_plan(Plan& p, int batch, int heads, int tokens, int head_dim, int globa
   p.key_blocks = tokens / 64;
   p.global_tiles = all_queries ? global_tokens / p.qt : 0;
   // A global query tile sweeps every key block.  It is split into at most MAX_SPLIT chunks of
-  // about the average work of one workgroup (at the nominal 2 workgroups x 256 CUs), and never
-  // shorter than the longest ordinary row: the chunks are claimed first, so each finishes well
-  // before the queues drain, while few chunks keep the partials and the merge small.
+  // about half the average work of one workgroup (at the nominal 2 workgroups x 256 CUs), and
+  // never shorter than the longest ordinary row or than MIN_CHUNK steps: the chunks are claimed
+  // first, so each finishes well before the queues drain, while few chunks keep the partials and
+  // the merge small.  The average is estimated from the table width, which overstates the row
+  // work by up to 2x for tables padded to a bound (rows paired on the device); half of it keeps
+  // the chunks short enough there and costs nothing on tables of exact width.
   const int64_t row_steps = (int64_t)width * p.kbr;
   const int64_t all_steps =
       (int64_t)batch * heads * ((int64_t)p.rows * row_steps + (int64_t)p.global_tiles * p.key_blocks);
-  int64_t target = (all_steps + NOMINAL_GROUPS - 1) / NOMINAL_GROUPS;
+  int64_t target = ((all_steps + NOMINAL_GROUPS - 1) / NOMINAL_GROUPS + 1) / 2;
   if (target < row_steps) target = row_steps;
+  if (target < MIN_CHUNK) target = MIN_CHUNK;
   int nsplit = (int)((p.key_blocks + target - 1) / target);
   nsplit = nsplit < 1 ? 1 : (nsplit > MAX_SPLIT ? MAX_SPLIT : nsplit);
   p.chunk = (p.key_blocks + nsplit - 1) / nsplit;
