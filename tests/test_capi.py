@@ -47,3 +47,35 @@ def test_qk_prep_rejections():
     assert call(normalize=1, eps=0.0) == 1
     assert call() == 1 and "null" in _lib.last_error()
     assert call(normalize=0, weight=16) == 1
+
+
+def _global_chunks(batch, heads, tokens, global_tokens, width, head_dim=128):
+    """Chunks per global query tile, read back from the workspace size of a paired launch.
+
+    The workspace is 256 bytes of queue counters plus, per chunk of each 128-query global tile,
+    the four waves' partial accumulators (head_dim/32 fragments x 16 x 64 fp32) and their
+    (max, sum) rows (128 fp32); an unsplit tile needs no partials.
+    """
+    lib = _lib.load()
+    ws = lib.hb_attention_workspace_bytes(batch, heads, tokens, head_dim, global_tokens, width,
+                                          64, 1, 1)
+    per_chunk = 4 * ((head_dim // 32) * 16 * 64 * 4 + 128 * 4)
+    tiles = batch * heads * (global_tokens // 128)
+    assert (ws - 256) % (tiles * per_chunk) == 0
+    return max(1, (ws - 256) // (tiles * per_chunk))
+
+
+def test_global_tile_split_plan():
+    # FLUX 2048 px 16-tile K3 (264 key blocks, 128 paired rows of at most 28 entries): three
+    # chunks of 88 blocks
+    assert _global_chunks(1, 24, 16896, 512, 28) == 3
+    # the same rows padded to twice the 64-query width (rows paired on the device without a host
+    # sync) still split: one 264-block item per global tile would outlast the ordinary rows
+    assert _global_chunks(1, 24, 16896, 512, 52) == 2
+    # 1024 px (72 key blocks): chunks never fall below 64 steps' worth of target, so two of 36
+    assert _global_chunks(1, 24, 4608, 512, 16) == 2
+    assert _global_chunks(1, 24, 4608, 512, 27) == 2
+    # a row as long as the whole key range leaves the global tiles unsplit
+    assert _global_chunks(1, 24, 4608, 512, 72) == 1
+    # 4096 px 16-tile K3 (1032 key blocks, width 75): two chunks of 516
+    assert _global_chunks(1, 24, 66048, 512, 75) == 2
