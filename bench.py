@@ -48,7 +48,8 @@ HEADS, DIM = 24, 128
 WEIGHTS = (15, 14, 14, 14)
 KERNEL_NAMES = {"paired": "attn_fwd_kernel<2,128,1,false> (hb_paired_fwd)",
                 "paired128": "attn_fwd_kernel<2,128,2,false> (hb_paired_fwd)",
-                "unpaired": "attn_fwd_kernel<1,128,1,false> (hb_block_sparse_fwd)"}
+                # pairable 64-query tables: pair_rows_kernel (hb_pair_rows) + the paired kernel
+                "unpaired": "attn_fwd_kernel<2,128,1,false> (hb_pair_rows + hb_paired_fwd)"}
 TABLE_NAMES = {"paired": "paired", "paired128": "paired KV128", "unpaired": "unpaired (sparse_attention)"}
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0

@@ -57,6 +57,7 @@ SIGNATURES = {
     "hb_table_bits": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _p, _p]),
     "hb_bits_counts": (_c_int, [_p, _c_int, _c_int, _c_int, _p, _p, _p, _p]),
     "hb_bits_emit": (_c_int, [_p, _c_int, _c_int, _c_int, _p, _c_int, _p, _p, _c_int, _p]),
+    "hb_pair_rows": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _p]),
 }
 
 _lib = None

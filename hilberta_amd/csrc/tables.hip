@@ -481,3 +481,75 @@ extern "C" int hb_bits_emit(const uint32_t* bits, int32_t rows, int32_t total_bl
   HB_HIP(hipGetLastError());
   return HB_OK;
 }
+
+// Pairs an unpaired table in one launch (pair_metadata, paired_metadata.py:26-51): one wave per
+// paired row r builds the key-block bitmaps of rows 2r and 2r + 1 in LDS, then writes their union
+// in ascending key-block order with flag bit (half + 2*key_half) set where row `half` holds key
+// half `key_half`, zero-pads the row to out_width and stores its count.  Ids outside [0, T) and
+// entries past a row's count (clamped to width) are ignored.
+constexpr int PAIR_MAX_BLOCKS = 2048;  // key blocks per row the LDS bitmaps cover
+constexpr int PAIR_WORDS = PAIR_MAX_BLOCKS / 32 + 2;
+__global__ __launch_bounds__(TPB) void pair_rows_kernel(const int32_t* ids, const int32_t* counts,
+                                                        int prows, int width, int T, int ratio,
+                                                        int out_width, int32_t* out_ids,
+                                                        int32_t* out_flags, int32_t* out_counts) {
+  __shared__ uint32_t bm[TPB / 64][2][PAIR_WORDS];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int pr = blockIdx.x * (TPB / 64) + w;
+  for (int i = lane; i < 2 * PAIR_WORDS; i += 64) bm[w][i / PAIR_WORDS][i % PAIR_WORDS] = 0u;
+  __syncthreads();
+  if (pr < prows) {
+    for (int h = 0; h < 2; ++h) {
+      const int row = 2 * pr + h;
+      const int c = min(max(counts[row], 0), width);
+      const int32_t* rid = ids + (int64_t)row * width;
+      for (int e = lane; e < c; e += 64) {
+        const int p = rid[e];
+        if (p >= 0 && p < T) atomicOr(&bm[w][h][p >> 5], 1u << (p & 31));
+      }
+    }
+  }
+  __syncthreads();
+  if (pr >= prows) return;
+  // pair_flag reads bit kb * ratio + kh <= T, inside the PAIR_WORDS words
+  const int nkb = (T + ratio - 1) / ratio;
+  int32_t* oid = out_ids + (int64_t)pr * out_width;
+  int32_t* ofl = out_flags + (int64_t)pr * out_width;
+  int base = 0;
+  for (int kb0 = 0; kb0 < nkb; kb0 += 64) {
+    const int kb = kb0 + lane;
+    const int flag = kb < nkb ? pair_flag(bm[w][0], bm[w][1], kb, ratio) : 0;
+    const uint64_t live = __ballot(flag != 0);
+    const int pos = base + __popcll(live & ((1ull << lane) - 1));
+    if (flag && pos < out_width) {
+      oid[pos] = kb;
+      ofl[pos] = flag;
+    }
+    base += __popcll(live);
+  }
+  const int cnt = min(base, out_width);
+  for (int e = cnt + lane; e < out_width; e += 64) {
+    oid[e] = 0;
+    ofl[e] = 0;
+  }
+  if (lane == 0) out_counts[pr] = cnt;
+}
+
+extern "C" int hb_pair_rows(const int32_t* kv_indices, const int32_t* kv_counts, int32_t rows,
+                            int32_t width, int32_t total_blocks, int32_t key_block_size,
+                            int32_t* paired_ids, int32_t* paired_flags, int32_t* paired_counts,
+                            int32_t paired_width, hb_stream_t stream) {
+  HB_REQUIRE(kv_indices && kv_counts && paired_ids && paired_flags && paired_counts,
+             "null pointer argument");
+  HB_REQUIRE(rows > 0 && rows % 2 == 0, "rows must be positive and even (got %d)", rows);
+  HB_REQUIRE(width > 0 && paired_width > 0, "table widths must be positive");
+  HB_REQUIRE(total_blocks > 0 && total_blocks <= PAIR_MAX_BLOCKS,
+             "total_blocks must be in [1, %d] (got %d)", PAIR_MAX_BLOCKS, total_blocks);
+  HB_REQUIRE(key_block_size == 64 || key_block_size == 128, "key_block_size must be 64 or 128");
+  const int prows = rows / 2, per_block = TPB / 64;
+  hipLaunchKernelGGL(pair_rows_kernel, dim3((prows + per_block - 1) / per_block), dim3(TPB), 0,
+                     stream, kv_indices, kv_counts, prows, width, total_blocks, key_block_size / 64,
+                     paired_width, paired_ids, paired_flags, paired_counts);
+  HB_HIP(hipGetLastError());
+  return HB_OK;
+}

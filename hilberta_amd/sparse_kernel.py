@@ -187,12 +187,13 @@ def _block_sparse_fwd(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, s
     2r, 2r + 1 are merged on the device, as pair_metadata does (paired_metadata.py:26-51), and run
     on hb_paired_fwd: a 128-query item then keeps two waves per SIMD busy where a 64-query item
     keeps one.  Every query sees the same key blocks in the same ascending order with the same
-    arithmetic; blocks of the other half are masked to exact zeros.  The merge runs three small
-    kernels into tables padded to min(2 * width, N / 64) entries, with no host synchronisation.
-    Otherwise the rows run as they are on hb_block_sparse_fwd.
+    arithmetic; blocks of the other half are masked to exact zeros.  The merge is one kernel
+    (hb_pair_rows) writing tables padded to min(2 * width, N / 64) entries, with no host
+    synchronisation; it covers up to 2048 key blocks (N <= 131072).  Otherwise the rows run as
+    they are on hb_block_sparse_fwd.
     """
     B, H, N, D = q.shape
-    if N % 128 == 0 and global_tokens % 128 == 0:
+    if N % 128 == 0 and global_tokens % 128 == 0 and N // 64 <= 2048:
         _paired_from_unpaired(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, scale_log2,
                               all_queries)
         return
@@ -214,15 +215,13 @@ def _block_sparse_fwd(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, s
 def _paired_from_unpaired(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, scale_log2,
                           all_queries):
     """Pair 64-query tables on the device and launch hb_paired_fwd (see _block_sparse_fwd)."""
-    from ._tables import emit_device, table_bits_device
+    from ._tables import pair_rows_device
 
     lib = _lib.load()
     B, H, N, D = q.shape
     blocks = N // 64
-    bits = table_bits_device(kv_indices, kv_counts, blocks)
     width = min(2 * kv_indices.shape[1], blocks)
-    t = emit_device(bits, blocks, unpaired=False, paired=True, key_block_size=64, paired_width=width)
-    ids, flags, counts = t["paired_indices"], t["paired_flags"], t["paired_counts"]
+    ids, flags, counts = pair_rows_device(kv_indices, kv_counts, blocks, paired_width=width)
     ws = attention_workspace(q.device, B, H, N, D, global_tokens, width, 64, paired=1,
                              all_queries=all_queries)
     strides = (ctypes.c_int64 * 12)(*_strides(q, k, v, out))

@@ -163,6 +163,16 @@ int hb_bits_emit(const uint32_t* bits, int32_t rows, int32_t total_blocks, int32
                  int32_t* ids, int32_t width, int32_t* paired_ids, int32_t* paired_flags,
                  int32_t paired_width, hb_stream_t stream);
 
+/* Pairs an unpaired table in one launch, replacing pair_metadata (paired_metadata.py:26-51) on the
+ * device: rows 2r and 2r + 1 of kv_indices [rows, width] (with kv_counts) become paired row r of
+ * paired_ids / paired_flags [rows/2, paired_width], ascending, flag bit (half + 2*key_half),
+ * zero-padded, and paired_counts [rows/2].  paired_width must bound every paired row's entries
+ * (min(2*width, key blocks) always does); total_blocks <= 2048.  No host synchronisation. */
+int hb_pair_rows(const int32_t* kv_indices, const int32_t* kv_counts, int32_t rows, int32_t width,
+                 int32_t total_blocks, int32_t key_block_size, int32_t* paired_ids,
+                 int32_t* paired_flags, int32_t* paired_counts, int32_t paired_width,
+                 hb_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

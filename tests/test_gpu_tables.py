@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from oracle import topology as T
-from tests.helpers import say
+from tests.helpers import oracle_paired, oracle_plan, say
 
 pytestmark = pytest.mark.gpu
 
@@ -176,3 +176,37 @@ def test_plan_layout_permutes_latents(hip_device):
     packed = permute_tokens(lat, dp.layout.image_order)
     assert torch.equal(packed, lat.index_select(1, dp.layout.image_order))
     assert torch.equal(unpermute_tokens(packed, dp.layout.inverse_image_order), lat)
+
+
+@pytest.mark.parametrize("name,phase,kb", [("1024_t16k3", 0, 64), ("1024_t16k3", 3, 64),
+                                           ("1024_t4k1", 1, 128), ("2048_t16k3", 2, 64),
+                                           ("2048_t4k1", 1, 128)])
+def test_pair_rows_equals_pair_metadata(hip_device, name, phase, kb):
+    """hb_pair_rows (one launch, padded width, no host sync) is bit-exact with pair_metadata."""
+    from hilberta_amd._tables import pair_rows_device
+
+    plan = oracle_plan(name)
+    p = plan["phases"][phase]
+    ref = oracle_paired(plan, phase, key_block_size=kb)
+    ids_np, counts_np = np.asarray(p["kv_indices"]), np.asarray(p["kv_counts"])
+    rows, width = ids_np.shape
+    blocks = plan["total_tokens"] // 64
+    pwidth = min(2 * width, -(-blocks // (kb // 64)))
+    # entries past each row's count hold garbage (an out-of-range id and a duplicate): ignored
+    noisy = ids_np.copy()
+    for r in range(rows):
+        c = int(counts_np[r])
+        if c < width:
+            noisy[r, c:] = blocks + 7 if r % 2 else ids_np[r, 0]
+    say(f"case pair_rows {name} phase {phase} KB{kb} width {pwidth}")
+    ids, flags, counts = pair_rows_device(torch.from_numpy(noisy).to(hip_device),
+                                          torch.from_numpy(counts_np).to(hip_device), blocks,
+                                          key_block_size=kb, paired_width=pwidth)
+    torch.cuda.synchronize()
+    ids, flags, counts = ids.cpu().numpy(), flags.cpu().numpy(), counts.cpu().numpy()
+    ref_ids, ref_flags, ref_counts = (np.asarray(ref[k]) for k in ("kv_indices", "kv_flags", "kv_counts"))
+    assert np.array_equal(counts, ref_counts)
+    rw = ref_ids.shape[1]
+    assert rw <= pwidth
+    assert np.array_equal(ids[:, :rw], ref_ids) and np.array_equal(flags[:, :rw], ref_flags)
+    assert not ids[:, rw:].any() and not flags[:, rw:].any()
