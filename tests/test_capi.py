@@ -79,3 +79,16 @@ def test_global_tile_split_plan():
     assert _global_chunks(1, 24, 4608, 512, 72) == 1
     # 4096 px 16-tile K3 (1032 key blocks, width 75): two chunks of 516
     assert _global_chunks(1, 24, 66048, 512, 75) == 2
+
+
+def test_pair_rows_rejections():
+    lib = _lib.load()
+    buf = ctypes.c_void_p(16)  # never dereferenced: every call below fails its argument checks
+    rc = lib.hb_pair_rows(buf, buf, 3, 4, 72, 64, buf, buf, buf, 8, None)
+    assert rc == 1 and "even" in _lib.last_error()
+    rc = lib.hb_pair_rows(buf, buf, 4, 4, 4096, 64, buf, buf, buf, 8, None)
+    assert rc == 1 and "total_blocks" in _lib.last_error()
+    rc = lib.hb_pair_rows(buf, buf, 4, 4, 72, 96, buf, buf, buf, 8, None)
+    assert rc == 1 and "key_block_size" in _lib.last_error()
+    rc = lib.hb_pair_rows(None, buf, 4, 4, 72, 64, buf, buf, buf, 8, None)
+    assert rc == 1 and "null" in _lib.last_error()
