@@ -464,9 +464,10 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   };
 
   // ------------------------------------------------------------------ main loop
-  // Every item's step 0 is live (its first key block is global, which both query halves see).
-  // The K/V prefetch runs one step ahead across item boundaries, and the next item's Q is
-  // loaded right after the last score MFMAs of the current item.
+  // Every item starts at its step 0 with that step's own flags (a 128-key entry whose first half
+  // neither query half sees is then computed fully masked).  The K/V prefetch runs one step
+  // ahead across item boundaries, and the next item's Q is loaded right after the last score
+  // MFMAs of the current item.
   const uint16_t* cur_k = k_base(cur);
   const uint16_t* cur_v = v_base(cur);
   // block and flags of the current step, computed while the step before it issued their loads
@@ -498,10 +499,12 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
       step_info(sn, c_kb, c_fl);
       dma_block(other, cur_k, cur_v, c_kb);
     } else if (nxt_idx >= 0) {
-      // step 0 of the next item: its first key block is global, seen by both query halves
+      // step 0 of the next item: a global chunk's blocks are seen by both query halves; a row's
+      // first entry carries its own flags (tables without a global prefix, or G = 0, may start
+      // with an entry only one half sees), sub-step 0 of it for 128-key blocks
       const Item nxt = decode(nxt_idx);
       c_kb = nxt.global ? nxt.first_block : __builtin_amdgcn_readlane(n_id, 0) * KBR;
-      c_fl = 3;
+      c_fl = nxt.global ? 3 : (HALVES == 2 ? __builtin_amdgcn_readlane(n_fl, 0) & 3 : 1);
       dma_block(other, k_base(nxt), v_base(nxt), c_kb);
     }
     const bool live = (fl >> half) & 1;

@@ -24,6 +24,10 @@ from ._workspace import attention_workspace
 
 LOG2E = 1.4426950408889634
 
+# Persistent workgroup count for the attention launches of sparse_attention; 0 lets the library
+# choose (2 per compute unit).
+NUM_GROUPS = 0
+
 
 def validate_metadata(
     kv_indices, kv_counts, *, tokens, global_tokens=768, block_size=64, require_global_prefix=True
@@ -206,7 +210,7 @@ def _block_sparse_fwd(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, s
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
         lse.data_ptr() if lse is not None else None, strides, B, H, N, D,
         1 if q.dtype == torch.float16 else 0, kv_indices.data_ptr(), kv_counts.data_ptr(), width,
-        global_tokens, 64, int(all_queries), scale_log2, ws.data_ptr(), ws.numel(), 0,
+        global_tokens, 64, int(all_queries), scale_log2, ws.data_ptr(), ws.numel(), NUM_GROUPS,
         _lib.stream_ptr(q.device),
     )
     _lib.check(rc, "hb_block_sparse_fwd")
@@ -229,7 +233,7 @@ def _paired_from_unpaired(q, k, v, out, lse, kv_indices, kv_counts, global_token
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
         lse.data_ptr() if lse is not None else None, strides, B, H, N, D,
         1 if q.dtype == torch.float16 else 0, ids.data_ptr(), flags.data_ptr(), counts.data_ptr(),
-        width, global_tokens, 64, int(all_queries), scale_log2, ws.data_ptr(), ws.numel(), 0,
+        width, global_tokens, 64, int(all_queries), scale_log2, ws.data_ptr(), ws.numel(), NUM_GROUPS,
         _lib.stream_ptr(q.device),
     )
     _lib.check(rc, "hb_paired_fwd")
