@@ -29,6 +29,11 @@ SIGNATURES = {
         [_p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _c_int,
          _c_int, _c_int, _c_f32, _p, _c_i64, _c_int, _p],
     ),
+    "hb_paired_fwd_noalloc": (
+        _c_int,
+        [_p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _c_int,
+         _c_int, _c_int, _c_f32, _c_int, _p],
+    ),
     "hb_block_sparse_fwd": (
         _c_int,
         [_p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p, _c_int, _c_int,

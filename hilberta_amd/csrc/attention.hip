@@ -31,6 +31,8 @@
 //  * Online softmax in exp2 with fp32 state (paired_kernel.py:82-93) and a lazy rescale; P is
 //    rounded to the input type before the PV product as in the reference; an optional fp32
 //    per-row logsumexp (natural log) is written as well.
+#include <mutex>
+
 #include "common.h"
 #include "../../include/hilberta_hip.h"
 
@@ -769,6 +771,12 @@ int make_plan(Plan& p, int batch, int heads, int tokens, int head_dim, int globa
   return HB_OK;
 }
 
+// Zeroes the work-queue counters (the first 256 bytes of a workspace) ahead of a launch.  A fill
+// kernel rather than hipMemsetAsync, so that a captured HIP graph replays it as a kernel node.
+__global__ __launch_bounds__(64) void clear_counters_kernel(int32_t* counters) {
+  counters[threadIdx.x] = 0;
+}
+
 template <int HALVES, int D, int KBR, bool F16>
 void launch(const AttnArgs& a, int groups, hipStream_t stream) {
   hipLaunchKernelGGL((attn_fwd_kernel<HALVES, D, KBR, F16>), dim3(groups), dim3(128 * HALVES), 0,
@@ -797,7 +805,8 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, float*
                   const int32_t* kv_flags, const int32_t* kv_counts, int32_t table_width,
                   int32_t global_tokens, int32_t key_block_size, int32_t paired,
                   int32_t all_queries, float scale_log2, void* workspace,
-                  int64_t workspace_bytes, int32_t num_groups, hipStream_t stream) {
+                  int64_t workspace_bytes, int32_t num_groups, hipStream_t stream,
+                  bool clear_counters = false) {
   Plan p;
   int rc = make_plan(p, batch, heads, tokens, head_dim, global_tokens, table_width, key_block_size,
                      paired, all_queries);
@@ -849,6 +858,10 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, float*
   int groups = num_groups > 0 ? num_groups : 2 * device_cu_count();
   if (groups > items) groups = (int)items;
   if (groups < 1) return HB_OK;
+  if (clear_counters) {
+    static_assert(QUEUES + 1 <= 64, "the counters fit the cleared 256 bytes");
+    hipLaunchKernelGGL(clear_counters_kernel, dim3(1), dim3(64), 0, stream, a.counters);
+  }
   if (paired) {
     if (p.kbr == 2) dispatch_d<2, 2>(a, head_dim, dtype == HB_DTYPE_F16, groups, stream);
     else dispatch_d<2, 1>(a, head_dim, dtype == HB_DTYPE_F16, groups, stream);
@@ -856,6 +869,38 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, float*
     dispatch_d<1, 1>(a, head_dim, dtype == HB_DTYPE_F16, groups, stream);
   }
   HB_HIP(hipGetLastError());
+  return HB_OK;
+}
+
+}  // namespace
+}  // namespace hb
+
+// Workspace of hb_paired_fwd_noalloc: the work-queue counters and the split partials live in this
+// array, one copy per device, held from the library's first use on a device until the process
+// ends.  Host code never passes `scratch` itself to a kernel (on the host it names a stand-in, not
+// device memory): it passes the device address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) unsigned char scratch[HB_NOALLOC_SCRATCH_BYTES];
+
+namespace hb {
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// Device address of `scratch` on the current device, looked up once per device.
+int scratch_address(void** out) {
+  int dev = 0;
+  HB_HIP(hipGetDevice(&dev));
+  HB_REQUIRE(dev >= 0 && dev < MAX_DEVICES, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    HB_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    HB_REQUIRE(p != nullptr && ((uintptr_t)p & 255) == 0, "scratch address lookup failed");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
   return HB_OK;
 }
 
@@ -899,4 +944,31 @@ extern "C" int hb_block_sparse_fwd(const void* q, const void* k, const void* v, 
                            kv_indices, nullptr, kv_counts, table_width, global_tokens, 64, 0,
                            all_queries, scale_log2, workspace, workspace_bytes, num_groups,
                            stream);
+}
+
+extern "C" int hb_paired_fwd_noalloc(const void* q, const void* k, const void* v, void* out,
+                                     float* lse, const int64_t* strides, int32_t batch,
+                                     int32_t heads, int32_t tokens, int32_t head_dim,
+                                     int32_t dtype, const int32_t* kv_indices,
+                                     const int32_t* kv_flags, const int32_t* kv_counts,
+                                     int32_t table_width, int32_t global_tokens,
+                                     int32_t key_block_size, int32_t all_queries, float scale_log2,
+                                     int32_t num_groups, hipStream_t stream) {
+  // the size check comes first: shapes beyond the static scratch are rejected before any HIP call
+  hb::Plan p;
+  int rc = hb::make_plan(p, batch, heads, tokens, head_dim, global_tokens, table_width,
+                         key_block_size, 1, all_queries);
+  if (rc) return rc;
+  const int64_t need = p.counters_bytes + p.part_bytes + p.ml_bytes;
+  HB_REQUIRE(need <= HB_NOALLOC_SCRATCH_BYTES,
+             "hb_paired_fwd_noalloc: these shapes need %lld bytes of scratch, the static scratch "
+             "holds %lld; use hb_paired_fwd with a caller workspace",
+             (long long)need, (long long)HB_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  rc = hb::scratch_address(&ws);
+  if (rc) return rc;
+  return hb::attention_fwd(q, k, v, out, lse, strides, batch, heads, tokens, head_dim, dtype,
+                           kv_indices, kv_flags, kv_counts, table_width, global_tokens,
+                           key_block_size, 1, all_queries, scale_log2, ws, HB_NOALLOC_SCRATCH_BYTES,
+                           num_groups, stream, /*clear_counters=*/true);
 }

@@ -58,6 +58,26 @@ int hb_paired_fwd(const void* q, const void* k, const void* v, void* out, float*
                   float scale_log2, void* workspace, int64_t workspace_bytes, int32_t num_groups,
                   hb_stream_t stream);
 
+/* Paired-table forward that allocates nothing.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory or pass a workspace (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments, checks and results as
+ * hb_paired_fwd, without workspace / workspace_bytes: the work-queue counters and the split
+ * partials live in a static device array of HB_NOALLOC_SCRATCH_BYTES per device, which the
+ * library holds from its first use on a device until the process ends.  Shapes whose workspace
+ * (hb_attention_workspace_bytes) exceeds that size are rejected with HB_EINVAL before any HIP
+ * call.  Every call clears the counters with a fill kernel on `stream` (no memset, no
+ * allocation, no hipFree).  All calls on one device share the one array: calls that may overlap
+ * in time on one device (different streams, or graphs replayed concurrently) race and must be
+ * serialised by the caller. */
+#define HB_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int hb_paired_fwd_noalloc(const void* q, const void* k, const void* v, void* out, float* lse,
+                          const int64_t* strides, int32_t batch, int32_t heads, int32_t tokens,
+                          int32_t head_dim, int32_t dtype, const int32_t* kv_indices,
+                          const int32_t* kv_flags, const int32_t* kv_counts,
+                          int32_t table_width, int32_t global_tokens, int32_t key_block_size,
+                          int32_t all_queries, float scale_log2, int32_t num_groups,
+                          hb_stream_t stream);
+
 /* Unpaired-table forward (64-query rows, no flags).  Replaces _block_sparse_fwd[grid](...) of
  * reference hilberta/sparse_kernel.py:315-339 (kernel :28-97); block_size must be 64. */
 int hb_block_sparse_fwd(const void* q, const void* k, const void* v, void* out, float* lse,

@@ -92,3 +92,23 @@ def test_pair_rows_rejections():
     assert rc == 1 and "key_block_size" in _lib.last_error()
     rc = lib.hb_pair_rows(None, buf, 4, 4, 72, 64, buf, buf, buf, 8, None)
     assert rc == 1 and "null" in _lib.last_error()
+
+
+def test_noalloc_rejects_shapes_beyond_its_scratch():
+    """hb_paired_fwd_noalloc refuses shapes whose workspace exceeds its static scratch, before any
+    HIP call; the limit is HB_NOALLOC_SCRATCH_BYTES (32 MiB)."""
+    lib = _lib.load()
+    limit = 32 << 20
+    # a 2048-token global prefix at 2048 px: 16 global tiles per head, split in two
+    need = lib.hb_attention_workspace_bytes(1, 24, 16896, 128, 2048, 24, 64, 1, 1)
+    assert need > limit
+    buf = ctypes.c_void_p(4096)  # never dereferenced: the call fails its size check first
+    strides = (ctypes.c_int64 * 12)(*([8] * 12))
+    rc = lib.hb_paired_fwd_noalloc(buf, buf, buf, buf, None, strides, 1, 24, 16896, 128, 0, buf, buf,
+                                   buf, 24, 2048, 64, 1, 1.0, 0, None)
+    msg = _lib.last_error()
+    assert rc == 1 and "scratch" in msg and str(need) in msg and str(limit) in msg
+    # the shape checks shared with hb_paired_fwd come first
+    rc = lib.hb_paired_fwd_noalloc(buf, buf, buf, buf, None, strides, 1, 24, 16896, 96, 0, buf, buf,
+                                   buf, 24, 512, 64, 1, 1.0, 0, None)
+    assert rc == 1 and "head_dim" in _lib.last_error()
