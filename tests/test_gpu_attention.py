@@ -2,7 +2,7 @@
 
 Inputs: Q/K/V drawn on the CPU from seed 2707 (q, k, v order, fp32 -> bf16), tables from the CPU
 oracle.  The fp32 reference runs on the CPU where it takes seconds (1024 px) and, for the 2048 px
-shapes, as the same torch fp32 code on the device for a sample of query tiles.
+shapes, as the same torch fp32 code on the device over every query row.
 """
 
 import numpy as np
@@ -231,43 +231,50 @@ def test_repeat_calls_bitwise_identical(hip_device):
         assert torch.equal(o, outs[0])
 
 
+_QKV_2048: dict = {}
+
+
+def _qkv_2048(plan, device):
+    """Seed-2707 Q/K/V of a 2048 px config on the device, drawn once per module."""
+    N = plan["total_tokens"]
+    if N not in _QKV_2048:
+        _QKV_2048.clear()
+        _QKV_2048[N] = tuple(x.to(device) for x in _qkv(plan))
+    return _QKV_2048[N]
+
+
+@pytest.mark.parametrize("phase", range(4))
 @pytest.mark.parametrize("name", ["2048_t16k3", "2048_t4k1"])
-def test_paired_2048_sampled_tiles(hip_device, name):
-    """2048 px: full GPU output vs the fp32 reference on every global tile and 24 sampled rows."""
+def test_paired_2048_full_output(hip_device, name, phase):
+    """2048 px, 24 heads, every query row (global and ordinary), output and LSE, against the
+    oracle's fp32 block formulation run on the device."""
     from hilberta_amd.paired_kernel import paired_attention
 
     plan = oracle_plan(name)
-    q, k, v = _qkv(plan)
-    qd, kd, vd = (x.to(hip_device) for x in (q, k, v))
-    G = plan["global_tokens"]
-    rng = np.random.default_rng(0)
-    for phase in (0, 3):
-        say(f"case paired {name} phase {phase}")
-        meta = device_paired(oracle_paired(plan, phase), hip_device)
-        lse = torch.empty(q.shape[:3], dtype=torch.float32, device=hip_device)
-        out = paired_attention(qd, kd, vd, meta, lse=lse)
-        torch.cuda.synchronize()
-        p = plan["phases"][phase]
-        nq = len(p["kv_counts"])
-        sample = sorted(set(rng.choice(nq, 24, replace=False).tolist()) | {0, nq - 1})
-        # global rows: every key, on the device in fp32
-        qf, kf, vf = qd.float(), kd.float(), vd.float()
-        s = torch.matmul(qf[:, :, :G], kf.transpose(-1, -2).contiguous()) * D**-0.5
-        gl = torch.logsumexp(s, -1)
-        go = torch.matmul(torch.softmax(s, -1), vf)
-        del s
-        compare(out[:, :, :G], lse[:, :, :G], go, gl, f"{name} phase {phase} global rows")
-        # sampled ordinary query blocks, block formulation of the oracle on the device
-        sub_ids = p["kv_indices"][sample]
-        sub_counts = p["kv_counts"][sample]
-        for j, row in enumerate(sample):
-            q0 = G + 64 * row
-            cols = torch.from_numpy(
-                (sub_ids[j, : sub_counts[j]][:, None] * 64 + np.arange(64)).reshape(-1)
-            ).to(hip_device)
-            s = torch.matmul(qf[:, :, q0 : q0 + 64], kf[:, :, cols].transpose(-1, -2).contiguous())
-            s = s * D**-0.5
-            rl = torch.logsumexp(s, -1)
-            ro = torch.matmul(torch.softmax(s, -1), vf[:, :, cols])
-            compare(out[:, :, q0 : q0 + 64], lse[:, :, q0 : q0 + 64], ro, rl,
-                    f"{name} phase {phase} row {row}")
+    qd, kd, vd = _qkv_2048(plan, hip_device)
+    say(f"case paired {name} phase {phase} full output")
+    meta = device_paired(oracle_paired(plan, phase), hip_device)
+    lse = torch.empty(qd.shape[:3], dtype=torch.float32, device=hip_device)
+    out = paired_attention(qd, kd, vd, meta, global_strategy="triton", num_warps=8, lse=lse)
+    torch.cuda.synchronize()
+    ref_o, ref_l = reference(qd, kd, vd, plan, phase, device=hip_device)
+    compare(out, lse, ref_o, ref_l, f"{name} phase {phase} all rows")
+
+
+@pytest.mark.parametrize("phase", range(4))
+def test_sparse_attention_2048_full_output(hip_device, phase):
+    """The unpaired entry on the headline config: 64-query tables paired on the device, every
+    row against the oracle's fp32 block formulation on the device."""
+    from hilberta_amd.sparse_kernel import sparse_attention
+
+    plan = oracle_plan("2048_t16k3")
+    qd, kd, vd = _qkv_2048(plan, hip_device)
+    p = plan["phases"][phase]
+    say(f"case sparse_attention 2048_t16k3 phase {phase} full output")
+    lse = torch.empty(qd.shape[:3], dtype=torch.float32, device=hip_device)
+    out = sparse_attention(qd, kd, vd, torch.from_numpy(p["kv_indices"]).to(hip_device),
+                           torch.from_numpy(p["kv_counts"]).to(hip_device),
+                           global_tokens=plan["global_tokens"], global_strategy="triton", lse=lse)
+    torch.cuda.synchronize()
+    ref_o, ref_l = reference(qd, kd, vd, plan, phase, device=hip_device)
+    compare(out, lse, ref_o, ref_l, f"sparse_attention 2048_t16k3 phase {phase} all rows")
