@@ -13,11 +13,14 @@ rebuilt on hand-written HIP kernels behind a C ABI (include/hilberta_hip.h):
                     gated-residual AdaLN pass, one HIP kernel each
   flux_model / sampling_layout
                     a FLUX-shaped denoiser step on these kernels and the sampling-scope layout
+  ops               the entry points as torch custom ops (torch.ops.hilberta_hip.*), with fake
+                    implementations for tracing
 
 The modules keep the reference package's call surface.  There is no CPU fallback: the HIP library
 (python -m hilberta_amd.build) and a GPU are required for every computation.
 """
 
+from . import ops
 from .bridge_k import bridge_k_plan
 
 __version__ = "0.1.0"

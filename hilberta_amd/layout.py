@@ -35,11 +35,21 @@ def index_select_rows(x, dim, index, *, out=None, error=None):
 
     ``error`` may be a device int32 scalar tensor that is set to 1 if an index was out of range
     (such rows are left unwritten); without it, indices are trusted (validated at plan setup).
+    Without ``out`` and ``error`` this is the operator ``torch.ops.hilberta_hip.gather_rows``.
     """
     _lib.require_gpu(x, index)
     dim = dim % x.ndim
     if index.dtype != torch.int64 or index.ndim != 1 or index.device != x.device:
         raise ValueError("index must be a 1-D int64 tensor on x's device")
+    if out is None and error is None:
+        from . import ops
+
+        return ops.gather_rows(x, dim, index)
+    return gather_into(x, dim, index, out=out, error=error)
+
+
+def gather_into(x, dim, index, *, out=None, error=None):
+    """The hb_gather_rows launch behind index_select_rows (arguments already checked there)."""
     inner = x.shape[dim + 1 :]
     row_elems = math.prod(inner)
     expect = 1

@@ -8,20 +8,16 @@ share K/V loads but keep their own masks and softmax denominators (flag bit half
 
 from __future__ import annotations
 
-import ctypes
 import math
 from numbers import Integral, Real
 
 import torch
 
-from . import _lib
-from ._workspace import attention_workspace
 from .sparse_kernel import (
     LOG2E,
     _check_lse,
     _check_vector_layout,
     _non_overlapping_strides,
-    _strides,
     _tensor_byte_span,
 )
 
@@ -31,21 +27,13 @@ NUM_GROUPS = 0
 
 
 def _paired_fwd(q, k, v, out, lse, metadata, scale_log2, all_queries):
-    """Launch hb_paired_fwd on the current stream (module-level so tests can patch it)."""
-    lib = _lib.load()
-    B, H, N, D = q.shape
-    G, kb = int(metadata.global_tokens), int(metadata.key_block_size)
-    width = metadata.kv_indices.shape[1]
-    ws = attention_workspace(q.device, B, H, N, D, G, width, kb, paired=1, all_queries=all_queries)
-    strides = (ctypes.c_int64 * 12)(*_strides(q, k, v, out))
-    rc = lib.hb_paired_fwd(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-        lse.data_ptr() if lse is not None else None, strides, B, H, N, D,
-        1 if q.dtype == torch.float16 else 0, metadata.kv_indices.data_ptr(),
-        metadata.kv_flags.data_ptr(), metadata.kv_counts.data_ptr(), width, G, kb,
-        int(all_queries), scale_log2, ws.data_ptr(), ws.numel(), NUM_GROUPS, _lib.stream_ptr(q.device),
-    )
-    _lib.check(rc, "hb_paired_fwd")
+    """Launch through the operator hilberta_hip::paired_fwd on the current stream (module-level so
+    tests can patch it)."""
+    from . import ops
+
+    ops.paired_fwd(q, k, v, out, lse, metadata.kv_indices, metadata.kv_flags, metadata.kv_counts,
+                   int(metadata.global_tokens), int(metadata.key_block_size), float(scale_log2),
+                   bool(all_queries), int(NUM_GROUPS))
 
 
 def paired_attention(

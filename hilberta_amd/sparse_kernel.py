@@ -13,14 +13,11 @@ The dense-mask oracle ``explicit_mask`` is correctness tooling and lives in orac
 
 from __future__ import annotations
 
-import ctypes
 import math
 from numbers import Integral, Real
 
 import torch
 
-from . import _lib
-from ._workspace import attention_workspace
 
 LOG2E = 1.4426950408889634
 
@@ -185,58 +182,13 @@ def _strides(q, k, v, out):
 
 def _block_sparse_fwd(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, scale_log2,
                       all_queries):
-    """Launch the unpaired tables on the current stream (module-level so tests can patch it).
+    """Launch through the operator hilberta_hip::sparse_fwd on the current stream (module-level
+    so tests can patch it).  Pairable tables (N and the global prefix multiples of 128) are paired
+    on the device and run on the paired kernel; see hilberta_amd.ops.sparse_fwd."""
+    from . import ops
 
-    When the 64-query rows pair up (N and the global prefix multiples of 128), consecutive rows
-    2r, 2r + 1 are merged on the device, as pair_metadata does (paired_metadata.py:26-51), and run
-    on hb_paired_fwd: a 128-query item then keeps two waves per SIMD busy where a 64-query item
-    keeps one.  Every query sees the same key blocks in the same ascending order with the same
-    arithmetic; blocks of the other half are masked to exact zeros.  The merge is one kernel
-    (hb_pair_rows) writing tables padded to min(2 * width, N / 64) entries, with no host
-    synchronisation; it covers up to 2048 key blocks (N <= 131072).  Otherwise the rows run as
-    they are on hb_block_sparse_fwd.
-    """
-    B, H, N, D = q.shape
-    if N % 128 == 0 and global_tokens % 128 == 0 and N // 64 <= 2048:
-        _paired_from_unpaired(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, scale_log2,
-                              all_queries)
-        return
-    lib = _lib.load()
-    width = kv_indices.shape[1]
-    ws = attention_workspace(q.device, B, H, N, D, global_tokens, width, 64, paired=0,
-                             all_queries=all_queries)
-    strides = (ctypes.c_int64 * 12)(*_strides(q, k, v, out))
-    rc = lib.hb_block_sparse_fwd(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-        lse.data_ptr() if lse is not None else None, strides, B, H, N, D,
-        1 if q.dtype == torch.float16 else 0, kv_indices.data_ptr(), kv_counts.data_ptr(), width,
-        global_tokens, 64, int(all_queries), scale_log2, ws.data_ptr(), ws.numel(), NUM_GROUPS,
-        _lib.stream_ptr(q.device),
-    )
-    _lib.check(rc, "hb_block_sparse_fwd")
-
-
-def _paired_from_unpaired(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, scale_log2,
-                          all_queries):
-    """Pair 64-query tables on the device and launch hb_paired_fwd (see _block_sparse_fwd)."""
-    from ._tables import pair_rows_device
-
-    lib = _lib.load()
-    B, H, N, D = q.shape
-    blocks = N // 64
-    width = min(2 * kv_indices.shape[1], blocks)
-    ids, flags, counts = pair_rows_device(kv_indices, kv_counts, blocks, paired_width=width)
-    ws = attention_workspace(q.device, B, H, N, D, global_tokens, width, 64, paired=1,
-                             all_queries=all_queries)
-    strides = (ctypes.c_int64 * 12)(*_strides(q, k, v, out))
-    rc = lib.hb_paired_fwd(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-        lse.data_ptr() if lse is not None else None, strides, B, H, N, D,
-        1 if q.dtype == torch.float16 else 0, ids.data_ptr(), flags.data_ptr(), counts.data_ptr(),
-        width, global_tokens, 64, int(all_queries), scale_log2, ws.data_ptr(), ws.numel(), NUM_GROUPS,
-        _lib.stream_ptr(q.device),
-    )
-    _lib.check(rc, "hb_paired_fwd")
+    ops.sparse_fwd(q, k, v, out, lse, kv_indices, kv_counts, int(global_tokens), float(scale_log2),
+                   bool(all_queries), int(NUM_GROUPS))
 
 
 def sparse_attention(

@@ -1,10 +1,12 @@
 """CPU property mocks: host-side guards of the kernel entry points, no GPU touched.
 
 Mirrors the reference's tests/test_sparse_kernel_contract.py and tests/test_paired_kernel_contract.py:
-duck-typed tensors carry shape/stride/pointer/device; the HIP launchers are patched out.
+host views (HostView) stand in for device tensors; the HIP launchers are patched out.
 """
 
+from dataclasses import dataclass, field
 from types import SimpleNamespace
+from typing import Optional
 from unittest.mock import MagicMock, patch
 
 import pytest
@@ -14,39 +16,40 @@ from hilberta_amd.paired_kernel import paired_attention
 from hilberta_amd.sparse_kernel import _check_inputs, sparse_attention, validate_metadata
 
 
-class TensorProperties:
-    def __init__(self, shape, strides=None, dtype=torch.bfloat16, pointer=1_000_000, device="cuda:0",
-                 requires_grad=False):
-        self.shape = tuple(shape)
-        self.ndim = len(shape)
-        self.dtype = dtype
-        self.device = torch.device(device)
-        self.is_cuda = self.device.type == "cuda"
-        self.requires_grad = requires_grad
-        self.pointer = pointer
-        if strides is None:
-            strides, running = [], 1
-            for size in reversed(shape):
-                strides.insert(0, running)
-                running *= size
-        self.strides = tuple(strides)
+@dataclass
+class HostView:
+    """A device tensor as the host-side checks see it, with no device memory behind it: sizes,
+    element strides, dtype, device, autograd flag and the base address (for alias checks).  The
+    stride arithmetic is delegated to a meta tensor of the same geometry."""
+
+    shape: tuple
+    strides: Optional[tuple] = None
+    dtype: torch.dtype = torch.bfloat16
+    address: int = 1 << 20
+    device: torch.device = field(default_factory=lambda: torch.device("cuda", 0))
+    requires_grad: bool = False
+
+    def __post_init__(self):
+        if self.strides is None:
+            self.strides = torch.empty(self.shape, device="meta").stride()
+
+    def _meta(self):
+        return torch.empty_strided(self.shape, self.strides, dtype=self.dtype, device="meta")
+
+    ndim = property(lambda self: len(self.shape))
+    is_cuda = property(lambda self: self.device.type == "cuda")
 
     def stride(self, dim=None):
-        return self.strides if dim is None else self.strides[dim]
+        return tuple(self.strides) if dim is None else self.strides[dim]
 
     def data_ptr(self):
-        return self.pointer
+        return self.address
 
     def element_size(self):
-        return 4 if self.dtype == torch.int32 else 2
+        return self._meta().element_size()
 
     def is_contiguous(self):
-        running = 1
-        for size, stride in zip(reversed(self.shape), reversed(self.strides)):
-            if size > 1 and stride != running:
-                return False
-            running *= size
-        return True
+        return self._meta().is_contiguous()
 
 
 SHAPE = (1, 2, 512, 128)
@@ -57,12 +60,12 @@ NATIVE = (131072, 128, 256, 1)
 @pytest.fixture
 def sp():
     return SimpleNamespace(
-        q=TensorProperties(SHAPE, NATIVE, pointer=1_000_000),
-        k=TensorProperties(SHAPE, pointer=2_000_000),
-        v=TensorProperties(SHAPE, NATIVE, pointer=3_000_000),
-        ids=TensorProperties((6, 5), dtype=torch.int32, pointer=4_000_000),
-        counts=TensorProperties((6,), dtype=torch.int32, pointer=5_000_000),
-        out=TensorProperties(SHAPE, NATIVE, pointer=6_000_000),
+        q=HostView(SHAPE, NATIVE, address=1_000_000),
+        k=HostView(SHAPE, address=2_000_000),
+        v=HostView(SHAPE, NATIVE, address=3_000_000),
+        ids=HostView((6, 5), dtype=torch.int32, address=4_000_000),
+        counts=HostView((6,), dtype=torch.int32, address=5_000_000),
+        out=HostView(SHAPE, NATIVE, address=6_000_000),
     )
 
 
@@ -75,18 +78,18 @@ def check(sp, **changes):
 
 def test_native_output_and_mixed_input_strides(sp):
     check(sp)
-    check(sp, out=TensorProperties(SHAPE, pointer=6_000_000))
+    check(sp, out=HostView(SHAPE, address=6_000_000))
 
 
 @pytest.mark.parametrize("source", ["q", "ids"])
 def test_input_and_metadata_alias_rejected(sp, source):
-    sp.out.pointer = getattr(sp, source).pointer
+    sp.out.address = getattr(sp, source).address
     with pytest.raises(ValueError, match="alias"):
         check(sp)
 
 
 def test_partial_alias_rejected(sp):
-    sp.out.pointer = sp.k.pointer + 1024
+    sp.out.address = sp.k.address + 1024
     with pytest.raises(ValueError, match="alias"):
         check(sp)
 
@@ -148,16 +151,16 @@ def test_sparse_launch_reaches_hip_launcher(sp):
 @pytest.fixture
 def pa():
     ns = SimpleNamespace(
-        q=TensorProperties(SHAPE, NATIVE, pointer=1_000_000),
-        k=TensorProperties(SHAPE, pointer=2_000_000),
-        v=TensorProperties(SHAPE, NATIVE, pointer=3_000_000),
-        out=TensorProperties(SHAPE, NATIVE, pointer=7_000_000),
+        q=HostView(SHAPE, NATIVE, address=1_000_000),
+        k=HostView(SHAPE, address=2_000_000),
+        v=HostView(SHAPE, NATIVE, address=3_000_000),
+        out=HostView(SHAPE, NATIVE, address=7_000_000),
     )
     ns.meta = SimpleNamespace(
         tokens=512, global_tokens=128, key_block_size=64,
-        kv_indices=TensorProperties((3, 5), dtype=torch.int32, pointer=4_000_000),
-        kv_flags=TensorProperties((3, 5), dtype=torch.int32, pointer=5_000_000),
-        kv_counts=TensorProperties((3,), dtype=torch.int32, pointer=6_000_000),
+        kv_indices=HostView((3, 5), dtype=torch.int32, address=4_000_000),
+        kv_flags=HostView((3, 5), dtype=torch.int32, address=5_000_000),
+        kv_counts=HostView((3,), dtype=torch.int32, address=6_000_000),
     )
     return ns
 
@@ -173,10 +176,10 @@ def test_paired_native_output(pa):
 
 def test_paired_alias_rejected(pa):
     for src in (pa.q, pa.k, pa.v, pa.meta.kv_indices, pa.meta.kv_flags, pa.meta.kv_counts):
-        pa.out.pointer = src.pointer
+        pa.out.address = src.address
         with pytest.raises(ValueError, match="alias"):
             pcall(pa)
-    pa.out.pointer = pa.k.pointer + 64
+    pa.out.address = pa.k.address + 64
     with pytest.raises(ValueError, match="alias"):
         pcall(pa)
 
@@ -225,7 +228,7 @@ def test_paired_metadata_checks(pa):
 
 
 def test_vector_alignment_required(pa):
-    pa.q.pointer = 1_000_002  # not 16-byte aligned
+    pa.q.address = 1_000_002  # not 16-byte aligned
     with pytest.raises(ValueError, match="16-byte"):
         pcall(pa)
 
