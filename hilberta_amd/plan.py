@@ -89,31 +89,33 @@ class AttentionPlan:
         )
 
     def manifest(self):
-        glob = self.global_tokens // self.block_size
-        return dict(
-            grid_size=self.grid_size,
-            tile_count=self.tile_count,
-            text_tokens=self.text_tokens,
-            shared_tokens=self.shared_tokens,
-            block_size=self.block_size,
-            bridge=self.bridge,
-            full=self.full,
-            image_order_sha256=hashlib.sha256(self.image_order.cpu().numpy().tobytes()).hexdigest(),
-            physical_original_blocks=self.physical_original_blocks.cpu().tolist(),
-            phases=[
-                dict(
-                    offset=p.offset,
-                    kv_count_min=int(p.kv_counts.min()),
-                    kv_count_max=int(p.kv_counts.max()),
-                    directed_entries=(
-                        glob * (self.total_tokens // self.block_size) + int(p.kv_counts.sum())
-                    )
-                    * self.block_size**2,
-                    bridge_original_blocks=p.bridge_original_blocks.cpu().tolist(),
-                )
-                for p in self.phases
-            ],
-        )
+        """JSON-ready summary in the reference's manifest format (plan.py:86-111): the geometry
+        fields, a SHA-256 of the image order's int64 bytes, the physical block packing and, per
+        phase, its offset, the range of row lengths, the directed (query, key) token entries
+        the tables admit and the chosen bridge blocks."""
+        bs = self.block_size
+        # every global query block sees every key block; ordinary rows see what they list
+        global_block_entries = (self.global_tokens // bs) * (self.total_tokens // bs)
+
+        def phase_summary(p):
+            counts = p.kv_counts.cpu()
+            listed = int(counts.sum())
+            return {
+                "offset": p.offset,
+                "kv_count_min": int(counts.min()),
+                "kv_count_max": int(counts.max()),
+                "directed_entries": (global_block_entries + listed) * bs * bs,
+                "bridge_original_blocks": p.bridge_original_blocks.cpu().tolist(),
+            }
+
+        fields = ("grid_size", "tile_count", "text_tokens", "shared_tokens", "block_size", "bridge",
+                  "full")
+        summary = {name: getattr(self, name) for name in fields}
+        summary["image_order_sha256"] = hashlib.sha256(
+            self.image_order.cpu().numpy().tobytes()).hexdigest()
+        summary["physical_original_blocks"] = self.physical_original_blocks.cpu().tolist()
+        summary["phases"] = [phase_summary(p) for p in self.phases]
+        return summary
 
 
 def _check_geometry(tile_count, grid_size, text_tokens, block_size):
@@ -187,15 +189,13 @@ def _to_attention_plan(layout, phases, tile_count, bridge, directed):
 
 
 def full_attention_plan(plan):
-    """Same persistent layout, all connections: permutation-equivalence gate (plan.py:200-212)."""
-    nb = plan.total_tokens // plan.block_size
-    nq = (plan.total_tokens - plan.global_tokens) // plan.block_size
-    ids = torch.arange(nb, dtype=torch.int32).repeat(nq, 1)
-    counts = torch.full((nq,), nb, dtype=torch.int32)
-    return replace(
-        plan,
-        phases=tuple(
-            replace(p, kv_indices=ids.clone(), kv_counts=counts.clone()) for p in plan.phases
-        ),
-        full=True,
-    )
+    """The same persistent layout with every ordinary query block listing every key block
+    (plan.py:200-212): the dense gate, equal to unmasked attention up to the permutation."""
+    key_blocks = plan.total_tokens // plan.block_size
+    rows = (plan.total_tokens - plan.global_tokens) // plan.block_size
+
+    def every_block(p):
+        ids = torch.arange(key_blocks, dtype=torch.int32).expand(rows, key_blocks).contiguous()
+        return replace(p, kv_indices=ids, kv_counts=torch.full((rows,), key_blocks, dtype=torch.int32))
+
+    return replace(plan, phases=tuple(every_block(p) for p in plan.phases), full=True)

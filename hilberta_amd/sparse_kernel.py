@@ -1,14 +1,15 @@
 """Exact block-sparse FLUX self-attention on a persistent token layout (unpaired tables).
 
 Drop-in for the reference module hilberta/sparse_kernel.py: the same call surface
-(``sparse_attention``, ``validate_metadata``, ``_check_inputs``, ``_tensor_byte_span``,
-``_non_overlapping_strides``) with the same host-side checks and error messages, launching the
-gfx950 HIP kernel ``hb_block_sparse_fwd`` instead of the Triton ``_block_sparse_fwd``.
+(``sparse_attention``, ``validate_metadata``, ``explicit_mask``, ``_check_inputs``,
+``_tensor_byte_span``, ``_non_overlapping_strides``) with the same host-side checks and error
+messages, launching the gfx950 HIP kernels (operator hilberta_hip::sparse_fwd) instead of the
+Triton ``_block_sparse_fwd``.
 
 Q/K/V are [batch, heads, tokens, head_dim] views; physical token order is a fully connected
 global prefix followed by ordinary 64-token query blocks, each listing its allowed key blocks.
 Inference only; launches are asynchronous on the current stream with no host synchronisation.
-The dense-mask oracle ``explicit_mask`` is correctness tooling and lives in oracle/attention.py.
+``explicit_mask`` builds the dense mask of a table for correctness checks; no kernel uses it.
 """
 
 from __future__ import annotations
@@ -85,6 +86,21 @@ def validate_metadata(
         "ordinary_directed_entries": ordinary_entries,
         "total_directed_entries": global_tokens * tokens + ordinary_entries,
     }
+
+
+def explicit_mask(kv_indices, kv_counts, *, tokens, global_tokens=768, block_size=64):
+    """Dense [tokens, tokens] boolean mask of unpaired CPU tables, for correctness checks only
+    (reference sparse_kernel.py:155-166; the kernels never build it).  The tables are validated
+    first; global query rows see every key, ordinary query block r the key blocks it lists."""
+    validate_metadata(kv_indices, kv_counts, tokens=tokens, global_tokens=global_tokens,
+                      block_size=block_size)
+    key_blocks, global_blocks = tokens // block_size, global_tokens // block_size
+    listed = torch.arange(kv_indices.shape[1])[None, :] < kv_counts[:, None].long()
+    row = torch.arange(kv_indices.shape[0])[:, None].expand(kv_indices.shape)
+    blocks = torch.zeros(key_blocks, key_blocks, dtype=torch.bool)
+    blocks[:global_blocks] = True
+    blocks[global_blocks + row[listed], kv_indices.long()[listed]] = True
+    return blocks.repeat_interleave(block_size, 0).repeat_interleave(block_size, 1)
 
 
 def _tensor_byte_span(tensor):
