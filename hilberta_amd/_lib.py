@@ -23,6 +23,7 @@ _c_int, _c_i64, _c_f32, _p = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, cty
 SIGNATURES = {
     "hb_last_error": (ctypes.c_char_p, []),
     "hb_version": (_c_int, []),
+    "hb_stream_capture_id": (_c_int, [_p, _p]),
     "hb_attention_workspace_bytes": (_c_i64, [_c_int] * 9),
     "hb_paired_fwd": (
         _c_int,
@@ -62,7 +63,7 @@ SIGNATURES = {
     "hb_table_bits": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _p, _p]),
     "hb_bits_counts": (_c_int, [_p, _c_int, _c_int, _c_int, _p, _p, _p, _p]),
     "hb_bits_emit": (_c_int, [_p, _c_int, _c_int, _c_int, _p, _c_int, _p, _p, _c_int, _p]),
-    "hb_pair_rows": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _p]),
+    "hb_pair_rows": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _p, _p]),
 }
 
 _lib = None
@@ -110,6 +111,13 @@ def check(rc: int, name: str) -> None:
 def stream_ptr(device) -> int:
     """Raw hipStream_t of torch's current stream on ``device``."""
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def capture_id(stream: int) -> int:
+    """Identifier of the graph capture the raw hipStream_t ``stream`` takes part in, 0 if none."""
+    out = ctypes.c_uint64(0)
+    check(load().hb_stream_capture_id(stream, ctypes.byref(out)), "hb_stream_capture_id")
+    return out.value
 
 
 def require_gpu(*tensors) -> None:

@@ -163,13 +163,16 @@ def table_bits_device(kv_indices, kv_counts, total_blocks):
     return bits
 
 
-def pair_rows_device(kv_indices, kv_counts, total_blocks, *, key_block_size=64, paired_width):
+def pair_rows_device(kv_indices, kv_counts, total_blocks, *, key_block_size=64, paired_width,
+                     overflow=None):
     """Pair an unpaired device table in one launch, without a host synchronisation.
 
     The device form of ``pair_metadata`` (reference hilberta/paired_metadata.py:26-51): rows 2r
     and 2r + 1 become paired row r, ascending, flag bit (half + 2*key_half), zero-padded to
-    ``paired_width``, which must bound every paired row's entry count (min(2 * width, key blocks)
-    always does).  Returns (ids, flags, counts) as int32 device tensors.
+    ``paired_width``, which should bound every paired row's entry count (min(2 * width, key
+    blocks) always does).  ``overflow`` may be a device int32 scalar tensor that is set to 1 when
+    some paired row had to be cut to ``paired_width`` entries.  Returns (ids, flags, counts) as
+    int32 device tensors.
     """
     device = kv_indices.device
     rows, width = kv_indices.shape
@@ -178,6 +181,8 @@ def pair_rows_device(kv_indices, kv_counts, total_blocks, *, key_block_size=64, 
     counts = torch.empty((rows // 2,), dtype=torch.int32, device=device)
     rc = _lib.load().hb_pair_rows(kv_indices.data_ptr(), kv_counts.data_ptr(), rows, width,
                                   total_blocks, key_block_size, ids.data_ptr(), flags.data_ptr(),
-                                  counts.data_ptr(), paired_width, _lib.stream_ptr(device))
+                                  counts.data_ptr(), paired_width,
+                                  overflow.data_ptr() if overflow is not None else None,
+                                  _lib.stream_ptr(device))
     _lib.check(rc, "hb_pair_rows")
     return ids, flags, counts

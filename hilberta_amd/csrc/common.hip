@@ -34,3 +34,12 @@ int device_cu_count() {
 extern "C" const char* hb_last_error(void) { return hb::g_error; }
 
 extern "C" int hb_version(void) { return HB_ABI_VERSION; }
+
+extern "C" int hb_stream_capture_id(hb_stream_t stream, uint64_t* capture_id) {
+  HB_REQUIRE(capture_id, "null pointer argument");
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  unsigned long long id = 0;
+  HB_HIP(hipStreamGetCaptureInfo(stream, &status, &id));
+  *capture_id = status == hipStreamCaptureStatusActive ? (uint64_t)id : 0;
+  return HB_OK;
+}

@@ -486,13 +486,15 @@ extern "C" int hb_bits_emit(const uint32_t* bits, int32_t rows, int32_t total_bl
 // paired row r builds the key-block bitmaps of rows 2r and 2r + 1 in LDS, then writes their union
 // in ascending key-block order with flag bit (half + 2*key_half) set where row `half` holds key
 // half `key_half`, zero-pads the row to out_width and stores its count.  Ids outside [0, T) and
-// entries past a row's count (clamped to width) are ignored.
+// entries past a row's count (clamped to width) are ignored.  A union longer than out_width is
+// cut to out_width entries and sets *overflow (when given) to 1.
 constexpr int PAIR_MAX_BLOCKS = 2048;  // key blocks per row the LDS bitmaps cover
 constexpr int PAIR_WORDS = PAIR_MAX_BLOCKS / 32 + 2;
 __global__ __launch_bounds__(TPB) void pair_rows_kernel(const int32_t* ids, const int32_t* counts,
                                                         int prows, int width, int T, int ratio,
                                                         int out_width, int32_t* out_ids,
-                                                        int32_t* out_flags, int32_t* out_counts) {
+                                                        int32_t* out_flags, int32_t* out_counts,
+                                                        int32_t* overflow) {
   __shared__ uint32_t bm[TPB / 64][2][PAIR_WORDS];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int pr = blockIdx.x * (TPB / 64) + w;
@@ -533,12 +535,13 @@ __global__ __launch_bounds__(TPB) void pair_rows_kernel(const int32_t* ids, cons
     ofl[e] = 0;
   }
   if (lane == 0) out_counts[pr] = cnt;
+  if (lane == 0 && base > out_width && overflow) atomicOr(overflow, 1);
 }
 
 extern "C" int hb_pair_rows(const int32_t* kv_indices, const int32_t* kv_counts, int32_t rows,
                             int32_t width, int32_t total_blocks, int32_t key_block_size,
                             int32_t* paired_ids, int32_t* paired_flags, int32_t* paired_counts,
-                            int32_t paired_width, hb_stream_t stream) {
+                            int32_t paired_width, int32_t* overflow, hb_stream_t stream) {
   HB_REQUIRE(kv_indices && kv_counts && paired_ids && paired_flags && paired_counts,
              "null pointer argument");
   HB_REQUIRE(rows > 0 && rows % 2 == 0, "rows must be positive and even (got %d)", rows);
@@ -549,7 +552,7 @@ extern "C" int hb_pair_rows(const int32_t* kv_indices, const int32_t* kv_counts,
   const int prows = rows / 2, per_block = TPB / 64;
   hipLaunchKernelGGL(pair_rows_kernel, dim3((prows + per_block - 1) / per_block), dim3(TPB), 0,
                      stream, kv_indices, kv_counts, prows, width, total_blocks, key_block_size / 64,
-                     paired_width, paired_ids, paired_flags, paired_counts);
+                     paired_width, paired_ids, paired_flags, paired_counts, overflow);
   HB_HIP(hipGetLastError());
   return HB_OK;
 }

@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define HB_ABI_VERSION 1
+#define HB_ABI_VERSION 2
 #define HB_DTYPE_BF16 0
 #define HB_DTYPE_F16 1
 
@@ -25,6 +25,11 @@ typedef struct ihipStream_t* hb_stream_t;
 
 const char* hb_last_error(void);
 int hb_version(void);
+
+/* Identifier of the graph capture `stream` is taking part in (hipStreamGetCaptureInfo), or 0 when
+ * it is not capturing.  No counterpart in the reference: callers that keep per-stream workspaces
+ * use it to give every captured graph a workspace of its own. */
+int hb_stream_capture_id(hb_stream_t stream, uint64_t* capture_id);
 
 /* ---------------------------------------------------------------- (c) block-sparse attention
  * Workspace needed by hb_paired_fwd / hb_block_sparse_fwd for these shapes (bytes, or -1 when
@@ -186,12 +191,14 @@ int hb_bits_emit(const uint32_t* bits, int32_t rows, int32_t total_blocks, int32
 /* Pairs an unpaired table in one launch, replacing pair_metadata (paired_metadata.py:26-51) on the
  * device: rows 2r and 2r + 1 of kv_indices [rows, width] (with kv_counts) become paired row r of
  * paired_ids / paired_flags [rows/2, paired_width], ascending, flag bit (half + 2*key_half),
- * zero-padded, and paired_counts [rows/2].  paired_width must bound every paired row's entries
- * (min(2*width, key blocks) always does); total_blocks <= 2048.  No host synchronisation. */
+ * zero-padded, and paired_counts [rows/2].  paired_width should bound every paired row's entries
+ * (min(2*width, key blocks) always does): a longer row is cut to paired_width entries and sets
+ * *overflow (device int32, may be NULL; never cleared here) to 1.  total_blocks <= 2048.  No host
+ * synchronisation. */
 int hb_pair_rows(const int32_t* kv_indices, const int32_t* kv_counts, int32_t rows, int32_t width,
                  int32_t total_blocks, int32_t key_block_size, int32_t* paired_ids,
                  int32_t* paired_flags, int32_t* paired_counts, int32_t paired_width,
-                 hb_stream_t stream);
+                 int32_t* overflow, hb_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -16,7 +16,7 @@ def test_library_exports_every_declared_symbol():
     missing = [name for name in declared if not hasattr(lib, name)]
     assert not missing, missing
     assert set(declared) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
-    assert lib.hb_version() == 1
+    assert lib.hb_version() == 2
 
 
 def test_workspace_size_and_rejections():
@@ -84,13 +84,13 @@ def test_global_tile_split_plan():
 def test_pair_rows_rejections():
     lib = _lib.load()
     buf = ctypes.c_void_p(16)  # never dereferenced: every call below fails its argument checks
-    rc = lib.hb_pair_rows(buf, buf, 3, 4, 72, 64, buf, buf, buf, 8, None)
+    rc = lib.hb_pair_rows(buf, buf, 3, 4, 72, 64, buf, buf, buf, 8, None, None)
     assert rc == 1 and "even" in _lib.last_error()
-    rc = lib.hb_pair_rows(buf, buf, 4, 4, 4096, 64, buf, buf, buf, 8, None)
+    rc = lib.hb_pair_rows(buf, buf, 4, 4, 4096, 64, buf, buf, buf, 8, None, None)
     assert rc == 1 and "total_blocks" in _lib.last_error()
-    rc = lib.hb_pair_rows(buf, buf, 4, 4, 72, 96, buf, buf, buf, 8, None)
+    rc = lib.hb_pair_rows(buf, buf, 4, 4, 72, 96, buf, buf, buf, 8, None, None)
     assert rc == 1 and "key_block_size" in _lib.last_error()
-    rc = lib.hb_pair_rows(None, buf, 4, 4, 72, 64, buf, buf, buf, 8, None)
+    rc = lib.hb_pair_rows(None, buf, 4, 4, 72, 64, buf, buf, buf, 8, None, None)
     assert rc == 1 and "null" in _lib.last_error()
 
 

@@ -79,3 +79,45 @@ def test_paired_step_graph_replays_match_eager(hip_device):
     for p in range(4):
         assert torch.equal(outs[p], eager2[p]), f"updated Q, phase {p} output"
         assert torch.equal(lses[p], eager2_lse[p]), f"updated Q, phase {p} lse"
+
+
+def test_two_graphs_on_one_capture_stream_replay_concurrently(hip_device):
+    """Graphs captured one after another on torch's shared capture stream get workspaces of
+    their own, so replaying them at the same time on two streams gives each its eager result."""
+    from hilberta_amd import _workspace
+    from hilberta_amd.paired_kernel import paired_attention
+
+    plan = oracle_plan("2048_t16k3")
+    N = plan["total_tokens"]
+    q, k, v = (x.to(hip_device) for x in A.seeded_qkv(1, 6, N, 128, seed=33))
+    metas = [device_paired(oracle_paired(plan, p), hip_device) for p in range(2)]
+    eager = [paired_attention(q, k, v, m) for m in metas]
+    outs = [torch.empty_like(q) for _ in metas]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for m, o in zip(metas, outs):
+            paired_attention(q, k, v, m, out=o)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    say("case two graphs captured on the shared capture stream")
+    before = set(_workspace._CACHE)
+    graphs = [torch.cuda.CUDAGraph() for _ in metas]
+    for g, m, o in zip(graphs, metas, outs):
+        with torch.cuda.graph(g):
+            paired_attention(q, k, v, m, out=o)
+    torch.cuda.synchronize()
+    new = [key for key in _workspace._CACHE if key not in before]
+    assert len(new) == 2 and new[0][1] == new[1][1] and new[0][2] != new[1][2] != 0
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for rep in range(4):
+        say(f"case concurrent replay {rep}")
+        for o in outs:
+            o.zero_()
+        torch.cuda.synchronize()
+        for g, s in zip(graphs, streams):
+            with torch.cuda.stream(s):
+                g.replay()
+        torch.cuda.synchronize()
+        for p in range(2):
+            assert torch.equal(outs[p], eager[p]), f"replay {rep} graph {p}"

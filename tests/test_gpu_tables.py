@@ -210,3 +210,27 @@ def test_pair_rows_equals_pair_metadata(hip_device, name, phase, kb):
     assert rw <= pwidth
     assert np.array_equal(ids[:, :rw], ref_ids) and np.array_equal(flags[:, :rw], ref_flags)
     assert not ids[:, rw:].any() and not flags[:, rw:].any()
+
+
+def test_pair_rows_reports_overflow(hip_device):
+    """A paired width below the widest union cuts those rows to the width and raises the
+    overflow word; the exact width (the widest union of pair_metadata) leaves it at zero."""
+    from hilberta_amd._tables import pair_rows_device
+
+    plan = oracle_plan("1024_t16k3")
+    p = plan["phases"][1]
+    ref = oracle_paired(plan, 1)
+    exact = ref["kv_indices"].shape[1]
+    ids = torch.from_numpy(np.asarray(p["kv_indices"])).to(hip_device)
+    counts = torch.from_numpy(np.asarray(p["kv_counts"])).to(hip_device)
+    blocks = plan["total_tokens"] // 64
+    for width, expect in ((exact, 0), (exact - 1, 1), (4, 1)):
+        say(f"case pair_rows overflow width {width}")
+        flag = torch.zeros((), dtype=torch.int32, device=hip_device)
+        pid, _, pct = pair_rows_device(ids, counts, blocks, paired_width=width, overflow=flag)
+        torch.cuda.synchronize()
+        assert int(flag) == expect, width
+        ref_counts = np.asarray(ref["kv_counts"])
+        assert np.array_equal(pct.cpu().numpy(), np.minimum(ref_counts, width))
+        assert np.array_equal(pid.cpu().numpy()[:, :width][ref_counts >= width],
+                              np.asarray(ref["kv_indices"])[ref_counts >= width, :width])
