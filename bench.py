@@ -118,6 +118,19 @@ def profiled_traffic(config):
     return None, None
 
 
+def profile_value(filename, key):
+    """A `key: value` figure from a committed rocprofv3 summary under profiles/, or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", filename)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(key + ":"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def live_blocks(meta):
     flags = meta.kv_flags.cpu()
     counts = meta.kv_counts.cpu()
@@ -445,6 +458,9 @@ def main():
                     help="denoiser attention modes to time (comma-separated subset of full,t4k1,t16k3)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 5 times (calibrates FETCH/WRITE_SIZE)")
+    ap.add_argument("--layout-probe", action="store_true",
+                    help="only run the permutation gathers ([B, n, 3072] and [B, n, 64] bf16) and "
+                    "the device table build of --config, 5 times each (for counter runs)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py runs on one GPU: --gpus {a.gpus} is not supported in this build "
@@ -465,6 +481,27 @@ def main():
 
     if a.denoiser:
         denoiser_bench(a)
+        return
+
+    if a.layout_probe:
+        from hilberta_amd.bridge_k import paired_plan_device
+        from hilberta_amd.layout import index_select_rows
+
+        dev = torch.device("cuda:0")
+        grid, tiles, k = CONFIGS[a.config]
+        plan = paired_plan_device(tiles, k, grid_size=grid, device=dev)
+        n = grid * grid
+        hid = torch.randn(a.batch, n, 3072, device=dev).to(torch.bfloat16)
+        lat = torch.randn(a.batch, n, 64, device=dev).to(torch.bfloat16)
+        outs = [torch.empty_like(hid), torch.empty_like(lat)]
+        for _ in range(5):
+            index_select_rows(hid, 1, plan.layout.image_order, out=outs[0])
+            index_select_rows(lat, 1, plan.layout.image_order, out=outs[1])
+        for _ in range(5):
+            paired_plan_device(tiles, k, grid_size=grid, device=dev)
+        torch.cuda.synchronize()
+        print(json.dumps({"layout_probe": a.config, "gathers": [list(hid.shape), list(lat.shape)],
+                          "repeats": 5}))
         return
 
     from hilberta_amd.bridge_k import paired_plan_device
@@ -603,11 +640,22 @@ def main():
                 ref = statistics.median(queued_time(lambda x=x, dim=dim: x.index_select(dim, order), 20,
                                                     stream, pad))
                 cp = statistics.median(queued_time(lambda x=x, y=y: y.copy_(x), 20, stream, pad))
-                perm[name] = dict(us=round(t * 1e3, 2), GBps=round(nbytes / (t * 1e-3) / 1e9, 1),
+                gbps = nbytes / (t * 1e-3) / 1e9
+                row_bytes = x[0].numel() * x.element_size() // x.shape[dim] if dim else x[0].numel() * x.element_size()
+                vec = next(w for w in (16, 8, 4, 2, 1) if row_bytes % w == 0)
+                # counters exist for the 2048 px gathers (profiles/gather_rows_2048_hbm_traffic.md)
+                traffic = (profile_value("gather_rows_2048_hbm_traffic.md",
+                                         f"traffic_bytes_per_launch[{name}]")
+                           if a.config.startswith("2048") and a.batch == 1 else None)
+                perm[name] = dict(us=round(t * 1e3, 2), GBps=round(gbps, 1),
                                   torch_index_select_us=round(ref * 1e3, 2),
                                   same_size_copy_us=round(cp * 1e3, 2),
                                   same_size_copy_GBps=round(2 * x.numel() * x.element_size()
-                                                            / (cp * 1e-3) / 1e9, 1))
+                                                            / (cp * 1e-3) / 1e9, 1),
+                                  roofline=dict(bound="hbm", kernel=f"gather_rows_kernel<{vec}>",
+                                                achieved=round(gbps, 1), peak=PEAK_HBM_GBS,
+                                                unit="GB/s", frac=round(gbps / PEAK_HBM_GBS, 4),
+                                                algorithmic_bytes=nbytes, traffic=traffic))
             del src, dst, pad
             extras = dict(
                 stream_copy_GBps=round(2 * (1 << 30) / (copy_ms * 1e-3) / 1e9, 1),
@@ -691,6 +739,16 @@ def main():
         "table_build_ms": round(table_ms, 3),
         "table_build_bytes": table_bytes,
         "table_build_GBps": round(table_bytes / (table_ms * 1e-3) / 1e9, 2),
+        # launch-latency-bound: ~35 kernels of a few microseconds moving kilobytes each
+        # (profiles/table_build_2048_t16k3_kernel_trace.md)
+        "table_build_roofline": dict(
+            bound="latency", achieved=round(table_bytes / (table_ms * 1e-3) / 1e9, 2),
+            peak=PEAK_HBM_GBS, unit="GB/s",
+            frac=round(table_bytes / (table_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 6),
+            traffic=(profile_value("table_build_2048_t16k3_kernel_trace.md", "traffic_bytes_per_plan")
+                     if a.config == "2048_t16k3" else None),
+            kernel_us=(profile_value("table_build_2048_t16k3_kernel_trace.md", "kernel_us_per_plan")
+                       if a.config == "2048_t16k3" else None)),
         "timed_wall_ms": round(wall_ms, 2),
         "roofline": {
             "bound": "mfma",
