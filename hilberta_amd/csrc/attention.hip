@@ -428,27 +428,55 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     l_run[g] = 0.f;
   }
 
-  // Epilogue of the current item: normalised output (and LSE), or, for a chunk of a split global
-  // tile, its partial (unnormalised acc, max, sum) in fragment order; merge_kernel combines the
-  // chunks after this kernel (the kernel boundary makes every partial visible on every XCD).
+  // Output of a finished item, packed in the input type, held until it is stored.  The stores of
+  // an item are deferred to the next item's first step, after its barrier: the hand-over waits
+  // for the next item's loads, and vector memory operations complete in issue order, so stores
+  // issued at the hand-over would hold up that wait and the step barrier's fence behind them.
+  // The address of a lane's output row is the item's (uniform) base plus a lane offset that
+  // never changes, so the pending state costs the packed values and the LSE only.  With 128-key
+  // blocks the extra registers would spill, so those tables store at the epilogue.
+  static_assert(NG == 1, "one pending output tile per wave");
+  constexpr bool DEFER_OUTPUT = KBR == 1;
+  const int o_lane = (wave * QW + ql) * a.o_sn + hl * 4;
+  const int l_lane = wave * QW + ql;
+  u32x2 ow[DT][4];
+  uint16_t* o_item = nullptr;
+  float* l_item = nullptr;
+  float l_val = 0.f;
+  bool out_pending = false;
+  auto flush_output = [&]() {
+    if (!out_pending) return;
+    out_pending = false;
+    uint16_t* op = o_item + o_lane;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) *(u32x2*)(op + dt * 32 + gq * 8) = ow[dt][gq];
+    if (l_item && hl == 0) l_item[l_lane] = l_val;
+  };
+
+  // Epilogue of the current item: normalised output (and LSE), held for flush_output, or, for a
+  // chunk of a split global tile, its partial (unnormalised acc, max, sum) in fragment order,
+  // stored here; merge_kernel combines the chunks after this kernel (the kernel boundary makes
+  // every partial visible on every XCD).
   auto epilogue = [&]() {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       const float l_tot = pair_sum(l_run[g]);
       const int q = cur.qfirst + wave * QW + g * 32 + ql;
-      uint16_t* op = a.o + (int64_t)cur.b * a.o_sb + (int64_t)cur.h * a.o_sh + (int64_t)q * a.o_sn + hl * 4;
-      float* lsep = a.lse ? a.lse + (int64_t)cur.bh * a.tokens + q : nullptr;
       if (!cur.global || a.nsplit == 1) {
         const float inv = 1.f / l_tot;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            u32x2 w = {pack2<F16>(acc[g][dt][gq * 4 + 0] * inv, acc[g][dt][gq * 4 + 1] * inv),
-                       pack2<F16>(acc[g][dt][gq * 4 + 2] * inv, acc[g][dt][gq * 4 + 3] * inv)};
-            *(u32x2*)(op + dt * 32 + gq * 8) = w;
-          }
-        if (lsep && hl == 0) *lsep = (m_run[g] + __log2f(l_tot)) * LN2;
+          for (int gq = 0; gq < 4; ++gq)
+            ow[dt][gq] = u32x2{pack2<F16>(acc[g][dt][gq * 4 + 0] * inv, acc[g][dt][gq * 4 + 1] * inv),
+                               pack2<F16>(acc[g][dt][gq * 4 + 2] * inv, acc[g][dt][gq * 4 + 3] * inv)};
+        o_item = a.o + (int64_t)cur.b * a.o_sb + (int64_t)cur.h * a.o_sh + (int64_t)cur.qfirst * a.o_sn;
+        l_item = a.lse ? a.lse + (int64_t)cur.bh * a.tokens + cur.qfirst : nullptr;
+        l_val = (m_run[g] + __log2f(l_tot)) * LN2;
+        out_pending = true;
+        if constexpr (!DEFER_OUTPUT) flush_output();
         continue;
       }
       // partial slots: (tile, chunk)-major, then the item's 32-query group wave * NG + g
@@ -509,6 +537,7 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
       c_fl = nxt.global ? 3 : (HALVES == 2 ? __builtin_amdgcn_readlane(n_fl, 0) & 3 : 1);
       dma_block(other, k_base(nxt), v_base(nxt), c_kb);
     }
+    flush_output();  // the previous item's output, behind this step's loads
     const bool live = (fl >> half) & 1;
     const bool q_next = cross && nxt_idx >= 0;
     {
@@ -631,7 +660,10 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
       return false;
     }
     epilogue();
-    if (nxt_idx < 0) return true;
+    if (nxt_idx < 0) {
+      flush_output();
+      return true;
+    }
     // Wait here, once per item, for the next item's Q (and with it its first K/V block): with
     // no load pending on qreg at the loop head, the steady-state steps keep their K/V prefetch in
     // flight across the whole compute of a step.
