@@ -437,7 +437,7 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   // blocks the extra registers would spill, so those tables store at the epilogue.
   static_assert(NG == 1, "one pending output tile per wave");
   constexpr bool DEFER_OUTPUT = KBR == 1;
-  const int o_lane = (wave * QW + ql) * a.o_sn + hl * 4;
+  const int o_lane = (wave * QW + ql) * a.o_sn + hl * 8;
   const int l_lane = wave * QW + ql;
   u32x2 ow[DT][4];
   uint16_t* o_item = nullptr;
@@ -447,11 +447,20 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   auto flush_output = [&]() {
     if (!out_pending) return;
     out_pending = false;
+    // Lanes l and l + 32 hold the two 8-byte halves of each 16-byte chunk of a row: one swap
+    // per pair of chunks hands lane l the whole even chunk and lane l + 32 the whole odd one, so
+    // each lane stores 16 bytes and a store covers 32 bytes of each of the wave's 32 rows.
     uint16_t* op = o_item + o_lane;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) *(u32x2*)(op + dt * 32 + gq * 8) = ow[dt][gq];
+      for (int gp = 0; gp < 2; ++gp) {
+        const u32x2 ea = ow[dt][2 * gp], ob = ow[dt][2 * gp + 1];
+        const auto x = __builtin_amdgcn_permlane32_swap(ea[0], ob[0], false, false);
+        const auto y = __builtin_amdgcn_permlane32_swap(ea[1], ob[1], false, false);
+        const unsigned x0 = x[0], x1 = x[1], y0 = y[0], y1 = y[1];
+        *(u32x4*)(op + dt * 32 + gp * 16) = u32x4{x0, y0, x1, y1};
+      }
     if (l_item && hl == 0) l_item[l_lane] = l_val;
   };
 
