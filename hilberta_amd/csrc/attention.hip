@@ -125,20 +125,6 @@ __device__ __forceinline__ float pair_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// acc + (lo + hi) of a packed pair of 16-bit values (v_dot2_f32_{bf16,f16} against (1, 1)).
-template <bool F16>
-__device__ __forceinline__ float dot2_sum(uint32_t pair, float acc) {
-  if constexpr (F16) {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const h2 one = {(_Float16)1.f, (_Float16)1.f};
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pair), one, acc, false);
-  } else {
-    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-    const b2 one = {(__bf16)1.f, (__bf16)1.f};
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, pair), one, acc, false);
-  }
-}
-
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
 // 16 bytes per lane from base + voffset + soffset (bytes) into LDS at dst + 16 * lane, as a
@@ -150,6 +136,19 @@ __device__ __forceinline__ void buffer_load_lds16(const void* base, uint16_t* ds
   const __amdgpu_buffer_rsrc_t rsrc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, BUFFER_WORD3);
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr)dst, 16, voffset, soffset, 0, 0);
+#endif
+}
+
+// Entry i of a table row of `width` int32 entries, or 0 past its end: a raw buffer load, whose
+// range check returns 0 out of range, addressed by a scalar base and a 32-bit lane offset (no
+// per-lane 64-bit pointer to keep in vector registers).
+__device__ __forceinline__ int row_entry(const int32_t* row, int width, int i) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t*>(row), 0, width * 4, BUFFER_WORD3);
+  return __builtin_amdgcn_raw_buffer_load_b32(rsrc, i * 4, 0, 0);
+#else
+  return 0;
 #endif
 }
 
@@ -282,13 +281,10 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     t_id = 0;
     t_fl = 0;
     if (!it.valid || it.global) return;
-    const int32_t* ids = a.indices + (int64_t)it.row * a.width;
-    const int32_t* fls = a.flags + (int64_t)it.row * a.width;
+    const int64_t row = (int64_t)it.row * a.width;
     cnt = a.counts[it.row];
-    if (lane < a.width) {
-      t_id = ids[lane];
-      if (HALVES == 2) t_fl = fls[lane];
-    }
+    t_id = row_entry(a.indices + row, a.width, lane);
+    if (HALVES == 2) t_fl = row_entry(a.flags + row, a.width, lane);
   };
 
   Item cur = decode(uniform(s_claim[0]));
@@ -314,10 +310,9 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     const int sub = s - e * KBR;
     if (e >= tbase + 64) {
       tbase = e & ~63;
-      const int ee = tbase + lane;
-      const bool ok = ee < a.width;
-      t_id = ok ? a.indices[(int64_t)cur.row * a.width + ee] : 0;
-      t_fl = (HALVES == 2 && ok) ? a.flags[(int64_t)cur.row * a.width + ee] : 0;
+      const int64_t row = (int64_t)cur.row * a.width;
+      t_id = row_entry(a.indices + row, a.width, tbase + lane);
+      t_fl = HALVES == 2 ? row_entry(a.flags + row, a.width, tbase + lane) : 0;
       // Wait here, inside the refill branch, for the entries read just below: left pending past
       // the branch, the waitcnt pass would stall the next LDS reads on every path (vmcnt(0)).
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -527,13 +522,16 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     // now overwrite
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
+    const int sn = next_live(s + 1);
+    const bool cross = sn >= cur.nsteps;
+    // The claimed item's table entries are loaded after this step's tile loads and output
+    // stores, where the held output registers are free, unless this step already crosses to it.
+    const bool meta_late = claiming && !cross;
     if (claiming) {
       claiming = false;
       nxt_idx = uniform(s_claim[0]);
-      load_meta(decode(nxt_idx), n_cnt, n_id, n_fl);
+      if (!meta_late) load_meta(decode(nxt_idx), n_cnt, n_id, n_fl);
     }
-    const int sn = next_live(s + 1);
-    const bool cross = sn >= cur.nsteps;
     if (!cross) {
       step_info(sn, c_kb, c_fl);
       dma_block(other, cur_k, cur_v, c_kb);
@@ -547,6 +545,7 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
       dma_block(other, k_base(nxt), v_base(nxt), c_kb);
     }
     flush_output();  // the previous item's output, behind this step's loads
+    if (meta_late) load_meta(decode(nxt_idx), n_cnt, n_id, n_fl);
     const bool live = (fl >> half) & 1;
     const bool q_next = cross && nxt_idx >= 0;
     {
@@ -639,16 +638,15 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
           pk[g][2 * t + 1] = pack8<F16>(f32x8{sc[g][t][8], sc[g][t][9], sc[g][t][10], sc[g][t][11],
                                               sc[g][t][12], sc[g][t][13], sc[g][t][14], sc[g][t][15]});
         }
-        // row sum of the rounded P that enters the PV product (two chains of dot2)
-        float l0 = 0.f, l1 = 0.f;
+        // Row sum of P in fp32, before rounding, as paired_kernel.py:90 takes it (four chains).
+        // A sum of the rounded P would make O's weights sum to exactly one but put up to 2^-9 of
+        // relative error into l, i.e. about 2e-3 into the LSE of a row dominated by one key.
+        float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          l0 = dot2_sum<F16>(pk[g][ks][0], l0);
-          l1 = dot2_sum<F16>(pk[g][ks][1], l1);
-          l0 = dot2_sum<F16>(pk[g][ks][2], l0);
-          l1 = dot2_sum<F16>(pk[g][ks][3], l1);
-        }
-        l_run[g] += l0 + l1;
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) ls[i & 3] += sc[g][t][i];
+        l_run[g] += (ls[0] + ls[1]) + (ls[2] + ls[3]);
       }
       // O^T += V^T P^T, V operands read PFV MFMAs ahead, each feeding NG MFMAs
 #pragma unroll
