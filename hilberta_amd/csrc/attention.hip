@@ -769,7 +769,8 @@ int make_plan(Plan& p, int batch, int heads, int tokens, int head_dim, int globa
               int key_block_size, int paired, int all_queries) {
   HB_REQUIRE(batch > 0 && heads > 0 && tokens > 0, "batch, heads and tokens must be positive");
   HB_REQUIRE(head_dim == 64 || head_dim == 128, "head_dim must be 64 or 128 (got %d)", head_dim);
-  HB_REQUIRE(width >= 1, "table width must be positive");
+  // (a table row is read through a buffer whose byte size is a 32-bit width * 4)
+  HB_REQUIRE(width >= 1 && width < (1 << 28), "table width must be in [1, 2^28) (got %d)", width);
   p.halves = paired ? 2 : 1;
   p.qt = 64 * p.halves;
   p.waves = 2 * p.halves;
