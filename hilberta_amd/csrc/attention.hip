@@ -208,10 +208,13 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   // then chunk), [total_g, total_g + total_r) the ordinary rows ((batch, head)-major).  Queue x
   // (= blockIdx % nq, the XCD of the round-robin dispatch) owns the x-th eighth of each list, so
   // the items running on one XCD share heads and neighbouring K/V tiles in its L2, and hands out
-  // its global chunks first (longest items first), then its rows.  Workgroups claim items from
-  // their own queue with an atomic counter and steal from the others once it is empty.  The claim
-  // for the item after next is issued at an item boundary and consumed one step later, so its
-  // latency hides behind compute; the last workgroup to leave resets the counters.
+  // its global chunks first (longest items first), then its rows.  The first 2*w items of a
+  // queue served by w workgroups are dealt out without atomics, items r and r + w to the
+  // workgroup of rank r (all workgroups hitting eight counters at once at the launch would
+  // serialise there); later items are claimed with the queue's atomic counter, and a workgroup
+  // whose queue is empty steals from the others.  The claim for the item after next is issued
+  // at an item boundary and consumed one step later, so its latency hides behind compute; the
+  // last workgroup to leave resets the counters.
   __shared__ int s_claim[2];
   const int nq = gridDim.x < QUEUES ? (int)gridDim.x : QUEUES;
   const int qx = blockIdx.x % nq;
@@ -227,20 +230,28 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     c -= gl;
     return c < r_lo(q + 1) - r_lo(q) ? total_g + r_lo(q) + c : -1;
   };
-  // tid 0 only: code of a claimed item, or -1 when every queue is drained.
+  // workgroups serving queue q, whose first 2 * dealt(q) items are dealt out
+  auto dealt = [&](int q) { return ((int)gridDim.x - q + nq - 1) / nq; };
+  // tid 0 only: code of a claimed item (counter value first_count of this workgroup's queue), or
+  // -1 when every queue is drained.
   auto claim_from = [&](int first_count) {
-    const int own = item_of(qx, first_count);
+    const int own = item_of(qx, 2 * dealt(qx) + first_count);
     if (own >= 0) return own;
     for (int t = 1; t < nq; ++t) {
       const int q = (qx + t) % nq;
-      const int c = item_of(q, atomicAdd(&a.counters[q], 1));
+      const int c = item_of(q, 2 * dealt(q) + atomicAdd(&a.counters[q], 1));
       if (c >= 0) return c;
     }
     return -1;
   };
   if (tid == 0) {
-    s_claim[0] = claim_from(atomicAdd(&a.counters[qx], 1));
-    s_claim[1] = claim_from(atomicAdd(&a.counters[qx], 1));
+    const int rank = blockIdx.x / nq;
+    int i0 = item_of(qx, rank), i1 = item_of(qx, rank + dealt(qx));
+    // a queue shorter than its dealt share: claim (steal) instead
+    if (i0 < 0) i0 = claim_from(atomicAdd(&a.counters[qx], 1));
+    if (i1 < 0) i1 = claim_from(atomicAdd(&a.counters[qx], 1));
+    s_claim[0] = i0;
+    s_claim[1] = i1;
   }
   __syncthreads();
 
