@@ -232,9 +232,14 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   };
   // workgroups serving queue q, whose first 2 * dealt(q) items are dealt out
   auto dealt = [&](int q) { return ((int)gridDim.x - q + nq - 1) / nq; };
+  // When every queue's items are all dealt out (small problems), there is nothing to claim: no
+  // atomics at all, rather than one per queue per workgroup to find every queue empty.
+  const bool all_dealt =
+      2 * ((int)gridDim.x / nq) >= (total_g + nq - 1) / nq + (total_r + nq - 1) / nq;
   // tid 0 only: code of a claimed item (counter value first_count of this workgroup's queue), or
   // -1 when every queue is drained.
   auto claim_from = [&](int first_count) {
+    if (all_dealt) return -1;
     const int own = item_of(qx, 2 * dealt(qx) + first_count);
     if (own >= 0) return own;
     for (int t = 1; t < nq; ++t) {
@@ -694,7 +699,7 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     t_fl = n_fl;
     tbase = 0;
     if (!cur.global) cur.nsteps = max(uniform(n_cnt), 1) * KBR;
-    if (tid == 0) pending = atomicAdd(&a.counters[qx], 1);
+    if (tid == 0 && !all_dealt) pending = atomicAdd(&a.counters[qx], 1);
     claiming = true;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
