@@ -24,7 +24,7 @@ from tests.helpers import compare, device_paired, say
 
 pytestmark = pytest.mark.gpu
 
-CASES = 24
+CASES = 48
 
 
 def _draw(case):
