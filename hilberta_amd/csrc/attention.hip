@@ -12,8 +12,9 @@
 //  * Persistent workgroups (2 per CU) claim items from 8 work queues, one per XCD (queue x =
 //    blockIdx % 8, the XCD under round-robin dispatch, owns a contiguous range of the item list),
 //    so items that share K/V blocks run under one L2; idle workgroups steal from other queues.
-//    Claims run one item ahead, and the next item's table entries, first K/V block and Q tile are
-//    prefetched while the current item finishes, so no claim or load latency sits between items.
+//    Each workgroup's first two items are dealt out without atomics; later claims run one item
+//    ahead, and the next item's table entries, first K/V block and Q tile are prefetched while
+//    the current item finishes.
 //  * Per 64-key block: the K and V tiles stream from HBM straight into one of two LDS stages
 //    (buffer loads to LDS, 16 bytes per lane, rows unpadded with an XOR chunk swizzle); the next
 //    block's loads are in flight while the current block is computed.  Table entries that neither
@@ -29,8 +30,9 @@
 //    wave-uniform branch around the masked case measured slower: the compiler's schedule of the
 //    common path degrades).
 //  * Online softmax in exp2 with fp32 state (paired_kernel.py:82-93) and a lazy rescale; P is
-//    rounded to the input type before the PV product as in the reference; an optional fp32
-//    per-row logsumexp (natural log) is written as well.
+//    rounded to the input type before the PV product and summed unrounded into the row
+//    normaliser, as in the reference; an optional fp32 per-row logsumexp (natural log) is written
+//    as well.
 #include <mutex>
 
 #include "common.h"
