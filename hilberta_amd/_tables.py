@@ -112,6 +112,45 @@ def phase_bits_device(layout: DeviceLayout, tile_count, phase, bridge_mode, k, s
     return bits, chosen
 
 
+def _bits_counts(bits, total_blocks, unpaired, paired, key_block_size):
+    """Row counts (unpaired and/or paired) of a bitmap and the widest rows, on the device."""
+    device = bits.device
+    rows = bits.shape[0]
+    i32 = dict(dtype=torch.int32, device=device)
+    counts = torch.empty(rows, **i32) if unpaired else None
+    pcounts = torch.empty(rows // 2, **i32) if paired else None
+    maxc = torch.zeros(2, **i32)
+    rc = _lib.load().hb_bits_counts(bits.data_ptr(), rows, total_blocks, key_block_size,
+                                    counts.data_ptr() if unpaired else None,
+                                    pcounts.data_ptr() if paired else None, maxc.data_ptr(),
+                                    _lib.stream_ptr(device))
+    _lib.check(rc, "hb_bits_counts")
+    return counts, pcounts, maxc
+
+
+def _bits_emit(bits, total_blocks, counts, pcounts, width, pwidth, unpaired, paired,
+               key_block_size):
+    """Ascending tables of a bitmap at the given widths (rows zero-padded)."""
+    device = bits.device
+    rows = bits.shape[0]
+    i32 = dict(dtype=torch.int32, device=device)
+    ids = torch.empty((rows, width), **i32) if unpaired else None
+    pids = torch.empty((rows // 2, pwidth), **i32) if paired else None
+    pflags = torch.empty((rows // 2, pwidth), **i32) if paired else None
+    rc = _lib.load().hb_bits_emit(bits.data_ptr(), rows, total_blocks, key_block_size,
+                                  ids.data_ptr() if unpaired else None, width,
+                                  pids.data_ptr() if paired else None,
+                                  pflags.data_ptr() if paired else None, pwidth,
+                                  _lib.stream_ptr(device))
+    _lib.check(rc, "hb_bits_emit")
+    out = {}
+    if unpaired:
+        out.update(kv_indices=ids, kv_counts=counts)
+    if paired:
+        out.update(paired_indices=pids, paired_flags=pflags, paired_counts=pcounts)
+    return out
+
+
 def emit_device(bits, total_blocks, *, unpaired=True, paired=False, key_block_size=64,
                 paired_width=None):
     """Tables from a bitmap: returns dict with ids/counts and/or paired ids/flags/counts (device).
@@ -120,36 +159,26 @@ def emit_device(bits, total_blocks, *, unpaired=True, paired=False, key_block_si
     paired tables are asked for with ``paired_width`` given: an upper bound on the paired row
     length, used as is (rows zero-padded to it), with no host synchronisation.
     """
-    device = bits.device
-    lib = _lib.load()
-    rows = bits.shape[0]
-    i32 = dict(dtype=torch.int32, device=device)
-    counts = torch.empty(rows, **i32) if unpaired else None
-    pcounts = torch.empty(rows // 2, **i32) if paired else None
-    maxc = torch.zeros(2, **i32)
-    stream = _lib.stream_ptr(device)
-    rc = lib.hb_bits_counts(bits.data_ptr(), rows, total_blocks, key_block_size,
-                            counts.data_ptr() if unpaired else None,
-                            pcounts.data_ptr() if paired else None, maxc.data_ptr(), stream)
-    _lib.check(rc, "hb_bits_counts")
+    counts, pcounts, maxc = _bits_counts(bits, total_blocks, unpaired, paired, key_block_size)
     if paired_width is not None and not unpaired:
         width, pwidth = 1, int(paired_width)
     else:
         width, pwidth = (max(x, 1) for x in maxc.tolist())  # setup-time sync: table widths
-    ids = torch.empty((rows, width), **i32) if unpaired else None
-    pids = torch.empty((rows // 2, pwidth), **i32) if paired else None
-    pflags = torch.empty((rows // 2, pwidth), **i32) if paired else None
-    rc = lib.hb_bits_emit(bits.data_ptr(), rows, total_blocks, key_block_size,
-                          ids.data_ptr() if unpaired else None, width,
-                          pids.data_ptr() if paired else None, pflags.data_ptr() if paired else None,
-                          pwidth, stream)
-    _lib.check(rc, "hb_bits_emit")
-    out = {}
-    if unpaired:
-        out.update(kv_indices=ids, kv_counts=counts)
-    if paired:
-        out.update(paired_indices=pids, paired_flags=pflags, paired_counts=pcounts)
-    return out
+    return _bits_emit(bits, total_blocks, counts, pcounts, width, pwidth, unpaired, paired,
+                      key_block_size)
+
+
+def emit_device_many(bits_list, total_blocks, *, unpaired=True, paired=False, key_block_size=64):
+    """emit_device over several bitmaps (the phases of a plan) with one host synchronisation for
+    all their table widths: every count launch is queued before the widths are read back, so the
+    device runs the phases back to back instead of draining between them."""
+    counted = [_bits_counts(b, total_blocks, unpaired, paired, key_block_size) for b in bits_list]
+    widths = torch.stack([m for _, _, m in counted]).tolist()  # setup-time sync: table widths
+    return [
+        _bits_emit(b, total_blocks, c, pc, max(w[0], 1), max(w[1], 1), unpaired, paired,
+                   key_block_size)
+        for b, (c, pc, _), w in zip(bits_list, counted, widths)
+    ]
 
 
 def table_bits_device(kv_indices, kv_counts, total_blocks):

@@ -16,7 +16,7 @@ import torch
 
 from .paired_metadata import PairedMetadata
 from .plan import _check_geometry, _device_plan, _to_attention_plan
-from ._tables import DeviceLayout, emit_device, layout_device, phase_bits_device
+from ._tables import DeviceLayout, emit_device_many, layout_device, phase_bits_device
 
 
 def _check_k(k):
@@ -60,11 +60,11 @@ def paired_plan_device(tiles=4, k=1, shared=False, *, grid_size=64, text_tokens=
     if N % 128 or G % 128 or key_block_size not in (64, 128):
         raise ValueError("Paired queries require N/global aligned to 128; KV must be 64/128")
     scratch = torch.empty(layout.image_blocks**2, dtype=torch.int32, device=layout.original_order.device)
-    metas = []
-    for phase in range(4):
-        bits, _ = phase_bits_device(layout, tiles, phase, 2, k, scratch)
-        t = emit_device(bits, layout.total_blocks, unpaired=False, paired=True,
-                        key_block_size=key_block_size)
-        metas.append(PairedMetadata(t["paired_indices"], t["paired_flags"], t["paired_counts"], N, G,
-                                    key_block_size))
+    # The four phases' launches queue back to back (the score scratch is reused in stream order)
+    # with one host read of their table widths.
+    bits = [phase_bits_device(layout, tiles, phase, 2, k, scratch)[0] for phase in range(4)]
+    tables = emit_device_many(bits, layout.total_blocks, unpaired=False, paired=True,
+                              key_block_size=key_block_size)
+    metas = [PairedMetadata(t["paired_indices"], t["paired_flags"], t["paired_counts"], N, G,
+                            key_block_size) for t in tables]
     return DevicePlan(layout, tiles, k, metas)

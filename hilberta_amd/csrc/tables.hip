@@ -214,25 +214,31 @@ __global__ void topk_kernel(int nb, int k, int offset_blocks, const int32_t* sco
 }
 
 // Base rows: word w of ordinary row r = globals (physical id < gb) | ordinary blocks whose tile
-// label equals that of the row's block (plan.py:173-183).
+// label equals that of the row's block (plan.py:173-183).  One lane per (row, key block): a wave
+// covers 64 key blocks of one row, ballots its bits and writes the two words (rows are laid out
+// in 64-lane spans, the tail lanes of a row's last span idle), so every label is computed once
+// per lane instead of 32 times in a serial loop per word.
 __global__ void base_bits_kernel(int nq, int words, int T, int gb, int text_blocks, int bs,
                                  int64_t off, int64_t n, int64_t width, const int64_t* packed,
                                  uint32_t* bits) {
-  const int64_t total = (int64_t)nq * words;
+  const int spans = (T + 63) / 64;  // 64-lane spans per row
+  const int64_t total = (int64_t)nq * spans * 64;
+  const int lane = threadIdx.x & 63;
+  // every lane of a wave runs the same number of iterations (total is a multiple of 64)
   for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * blockDim.x) {
-    const int r = (int)(idx / words), w = (int)(idx % words);
-    const int64_t o = packed[gb - text_blocks + r];
-    const int lab = tile_label(o * bs, off, n, width);
-    uint32_t word = 0;
-    for (int bit = 0; bit < 32; ++bit) {
-      const int p = w * 32 + bit;
-      if (p >= T) break;
-      bool on;
-      if (p < gb) on = true;
-      else on = tile_label(packed[p - text_blocks] * bs, off, n, width) == lab;
-      word |= (uint32_t)on << bit;
+    const int64_t span = idx >> 6;
+    const int r = (int)(span / spans), sp = (int)(span % spans);
+    const int p = sp * 64 + lane;
+    bool on = false;
+    if (p < gb) {
+      on = true;
+    } else if (p < T) {
+      const int lab = tile_label(packed[gb - text_blocks + r] * bs, off, n, width);
+      on = tile_label(packed[p - text_blocks] * bs, off, n, width) == lab;
     }
-    bits[idx] = word;
+    const uint64_t m = __ballot(on);
+    const int w = sp * 2 + (lane >> 5);
+    if ((lane & 31) == 0 && w < words) bits[(int64_t)r * words + w] = (uint32_t)(m >> (lane & 32));
   }
 }
 
@@ -411,7 +417,7 @@ extern "C" int hb_plan_phase_bits(const int64_t* inverse_original,
   const int words = (T + 31) / 32;
   const int64_t width = n / tile_count;
   const int64_t off = phase * (width / 4);
-  hipLaunchKernelGGL(base_bits_kernel, dim3(grid_for((int64_t)nq * words)), dim3(TPB), 0, stream, nq,
+  hipLaunchKernelGGL(base_bits_kernel, dim3(grid_for((int64_t)nq * ((T + 63) / 64) * 64)), dim3(TPB), 0, stream, nq,
                      words, T, gb, text_blocks, block_size, off, n, width, physical_original_blocks,
                      bits);
   if (bridge_mode) {

@@ -14,7 +14,7 @@ from dataclasses import dataclass, replace
 
 import torch
 
-from ._tables import emit_device, layout_device, phase_bits_device
+from ._tables import emit_device_many, layout_device, phase_bits_device
 
 
 @dataclass(frozen=True)
@@ -145,12 +145,11 @@ def _device_plan(tile_count, grid_size, text_tokens, shared, bridge_mode, k, blo
         scratch = torch.empty(layout.image_blocks**2, dtype=torch.int32,
                               device=layout.original_order.device)
     width = grid_size**2 // tile_count
-    phases = []
-    for phase in range(4):
-        bits, chosen = phase_bits_device(layout, tile_count, phase, bridge_mode, k, scratch)
-        tables = emit_device(bits, layout.total_blocks, unpaired=True)
-        phases.append((phase * (width // 4), bits, tables, chosen))
-    return layout, phases
+    built = [phase_bits_device(layout, tile_count, phase, bridge_mode, k, scratch)
+             for phase in range(4)]
+    tables = emit_device_many([b for b, _ in built], layout.total_blocks, unpaired=True)
+    return layout, [(phase * (width // 4), bits, t, chosen)
+                    for phase, ((bits, chosen), t) in enumerate(zip(built, tables))]
 
 
 def build_plan(tile_count=4, grid_size=64, text_tokens=512, shared=True, bridge=True, block_size=64,
