@@ -624,7 +624,9 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
         for (int i = 0; i < 16; ++i) m = fmaxf(m, sc[g][1][i]);
         // A block this wave's query half may not see (paired flags) is computed but masked: its
         // row max counts as -inf (no rescale) and its exponent offset is -inf, so P = 0 exactly.
-        mx[g] = live ? pair_max(m) * a.scale_log2 : -__builtin_inff();
+        // This lane's max over its 32 keys of the row decides; the row max (with the other 32
+        // keys, held by the lane 32 away, which sees the same test) is taken only to rescale.
+        mx[g] = live ? m * a.scale_log2 : -__builtin_inff();
         resc |= mx[g] > m_run[g] + RESCALE_LOG2;
       }
       // Lazy rescale: the exponent reference m_run moves only when some row's max exceeds it by
@@ -633,7 +635,7 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
       if (__ballot(resc) != 0) {
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-          const float m_new = fmaxf(m_run[g], mx[g]);
+          const float m_new = fmaxf(m_run[g], pair_max(mx[g]));
           const float alpha = fast_exp2(m_run[g] - m_new);
           l_run[g] *= alpha;
 #pragma unroll
