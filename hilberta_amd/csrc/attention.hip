@@ -208,7 +208,7 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   // ------------------------------------------------------------------ persistent work queues
   // Item codes: [0, total_g) are the chunks of global query tiles ((batch, head)-major, then tile,
   // then chunk), [total_g, total_g + total_r) the ordinary rows ((batch, head)-major).  Queue x
-  // (= blockIdx % nq, the XCD of the round-robin dispatch) owns the x-th eighth of each list, so
+  // (= blockIdx % 8, the XCD of the round-robin dispatch) owns the x-th eighth of each list, so
   // the items running on one XCD share heads and neighbouring K/V tiles in its L2, and hands out
   // its global chunks first (longest items first), then its rows.  The first 2*w items of a
   // queue served by w workgroups are dealt out without atomics, items r and r + w to the
@@ -216,9 +216,11 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   // serialise there); later items are claimed with the queue's atomic counter, and a workgroup
   // whose queue is empty steals from the others.  The claim for the item after next is issued
   // at an item boundary and consumed one step later, so its latency hides behind compute; the
-  // last workgroup to leave resets the counters.
+  // last workgroup to leave resets the counters.  The queue count is a constant, so the queue
+  // arithmetic is shifts and masks (a grid of fewer than eight workgroups leaves some queues
+  // without workgroups of their own; their items are stolen).
   __shared__ int s_claim[2];
-  const int nq = gridDim.x < QUEUES ? (int)gridDim.x : QUEUES;
+  constexpr int nq = QUEUES;
   const int qx = blockIdx.x % nq;
   const int gper = a.global_tiles * a.nsplit;  // global chunks per (batch, head)
   const int total_g = a.bh * gper;
