@@ -71,7 +71,7 @@ struct AttnArgs {
   int32_t heads, tokens, bh, width, rows, key_blocks;
   int32_t global_tiles, nsplit, chunk, per_bh;
   float scale_log2;
-  int32_t* counters;  // [0, 8) queue heads, [8] exit count; zero between launches
+  int32_t* counters;  // [0, 8) queue heads, [8] exit count, [9] drained-queue mask; zero between launches
   float* part;        // split partial accumulators, fragment order
   float* part_ml;     // split partial (max, sum) per query lane
 };
@@ -246,8 +246,13 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
     if (all_dealt) return -1;
     const int own = item_of(qx, 2 * dealt(qx) + first_count);
     if (own >= 0) return own;
+    // The own queue is drained: mark it in the launch's drained-queue mask and skip the queues
+    // already marked, so the claim that finds every queue empty takes two round trips, not eight.
+    unsigned* mask = (unsigned*)&a.counters[QUEUES + 1];
+    const unsigned drained = atomicOr(mask, 1u << qx);
     for (int t = 1; t < nq; ++t) {
       const int q = (qx + t) % nq;
+      if ((drained >> q) & 1) continue;
       const int c = item_of(q, 2 * dealt(q) + atomicAdd(&a.counters[q], 1));
       if (c >= 0) return c;
     }
@@ -725,7 +730,7 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   // the last workgroup to leave resets the queue counters for the next launch
   __syncthreads();
   if (tid == 0 && atomicAdd(&a.counters[QUEUES], 1) == (int)gridDim.x - 1) {
-    for (int q = 0; q <= QUEUES; ++q) atomicExch(&a.counters[q], 0);
+    for (int q = 0; q <= QUEUES + 1; ++q) atomicExch(&a.counters[q], 0);
   }
 }
 
@@ -921,7 +926,7 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, float*
   if (groups > items) groups = (int)items;
   if (groups < 1) return HB_OK;
   if (clear_counters) {
-    static_assert(QUEUES + 1 <= 64, "the counters fit the cleared 256 bytes");
+    static_assert(QUEUES + 2 <= 64, "the counters fit the cleared 256 bytes");
     hipLaunchKernelGGL(clear_counters_kernel, dim3(1), dim3(64), 0, stream, a.counters);
   }
   if (paired) {
