@@ -1,5 +1,6 @@
-"""GPU edge cases of the attention path: table padding, the C ABI's all_queries=0 mode, 4096 px,
-B=2 with BNHD views and 128-key tables at 2048 px, and the permutation at 4096 px sizes.
+"""GPU edge cases of the attention path: table padding, the C ABI's all_queries=0 mode, 4096 px
+(sampled rows, and every row of all four phases), B=2 with BNHD views and 128-key tables at
+2048 px, and the permutation at 4096 px sizes.
 
 References are the fp32 oracle formulations in oracle/attention.py (block form on sampled query
 tiles, computed on the device in fp32), the kernel's own all_queries=1 output (bitwise), and
@@ -113,6 +114,56 @@ def test_paired_4096_sampled_rows(hip_device):
     nq = len(plan["phases"][phase]["kv_counts"])
     rows = sorted(set(np.random.default_rng(2).choice(nq, 12, replace=False).tolist()) | {0, nq - 1})
     _sampled_rows_check(out, lse, q, k, v, plan, phase, rows, "4096")
+
+
+_QKV_4096: dict = {}
+
+
+def _block_reference_all_heads(qd, kd, vd, plan, phase):
+    """oracle.attention.block_sparse_attention's block formulation in fp32 on the device, with
+    each 64-query row computed for every head in one batched product (the oracle loops over
+    heads, which at 4096 px means 24k small launches per phase)."""
+    G = plan["global_tokens"]
+    p = plan["phases"][phase]
+    qf, kf, vf = qd.float(), kd.float(), vd.float()
+    ref_o = torch.empty_like(qf)
+    ref_l = torch.empty(qf.shape[:3], dtype=torch.float32, device=qf.device)
+    for h0 in range(0, qf.shape[1], 6):
+        hs = slice(h0, h0 + 6)
+        s = torch.matmul(qf[:, hs, :G], kf[:, hs].transpose(-1, -2).contiguous()) * D**-0.5
+        ref_l[:, hs, :G] = torch.logsumexp(s, -1)
+        ref_o[:, hs, :G] = torch.matmul(torch.softmax(s, -1), vf[:, hs])
+        del s
+    ids_all = torch.from_numpy(p["kv_indices"].astype(np.int64)).to(qd.device)
+    for row, count in enumerate(p["kv_counts"].tolist()):
+        q0 = G + 64 * row
+        cols = (ids_all[row, :count, None] * 64 + torch.arange(64, device=qd.device)).reshape(-1)
+        s = torch.matmul(qf[:, :, q0 : q0 + 64], kf[:, :, cols].transpose(-1, -2).contiguous())
+        s = s * D**-0.5
+        ref_l[:, :, q0 : q0 + 64] = torch.logsumexp(s, -1)
+        ref_o[:, :, q0 : q0 + 64] = torch.matmul(torch.softmax(s, -1), vf[:, :, cols])
+    return ref_o, ref_l
+
+
+@pytest.mark.parametrize("phase", range(4))
+def test_paired_4096_full_output(hip_device, phase):
+    """4096 px 16-tile K3 (N = 66048, the largest config), 24 heads: every query row of the
+    phase, output and LSE, against the block formulation in fp32 on the device."""
+    from hilberta_amd.paired_kernel import paired_attention
+
+    plan = oracle_plan("4096_t16k3")
+    N = plan["total_tokens"]
+    if N not in _QKV_4096:
+        _QKV_4096.clear()
+        _QKV_4096[N] = tuple(x.to(hip_device) for x in A.seeded_qkv(1, 24, N, D, seed=2707))
+    q, k, v = _QKV_4096[N]
+    say(f"case paired 4096_t16k3 phase {phase} full output")
+    meta = device_paired(oracle_paired(plan, phase), hip_device)
+    lse = torch.empty(1, 24, N, dtype=torch.float32, device=hip_device)
+    out = paired_attention(q, k, v, meta, global_strategy="triton", lse=lse)
+    torch.cuda.synchronize()
+    ref_o, ref_l = _block_reference_all_heads(q, k, v, plan, phase)
+    compare(out, lse, ref_o, ref_l, f"4096_t16k3 phase {phase} all rows")
 
 
 def test_paired_2048_batch2_bnhd_key_block_128(hip_device):
