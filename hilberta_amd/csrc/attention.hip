@@ -215,8 +215,9 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   // workgroup of rank r (all workgroups hitting eight counters at once at the launch would
   // serialise there); later items are claimed with the queue's atomic counter, and a workgroup
   // whose queue is empty steals from the others.  The claim for the item after next is issued
-  // at an item boundary and consumed one step later, so its latency hides behind compute; the
-  // last workgroup to leave resets the counters.  The queue count is a constant, so the queue
+  // at an item boundary, after the wait for the next item's loads, and read at the top of that
+  // item's first step (its table entries are loaded during that step); the last workgroup to
+  // leave resets the counters.  The queue count is a constant, so the queue
   // arithmetic is shifts and masks (a grid of fewer than eight workgroups leaves some queues
   // without workgroups of their own; their items are stolen).
   __shared__ int s_claim[2];
@@ -750,6 +751,45 @@ __global__ __launch_bounds__(128 * HALVES) void merge_kernel(AttnArgs a) {
   const int bh = tile / a.global_tiles, gtile = tile - bh * a.global_tiles;
   const int b = bh / a.heads, h = bh - b * a.heads;
   const int64_t sl0 = (int64_t)tile * a.nsplit * WAVES + wave;
+  const int q = gtile * QT + wave * 32 + ql;
+  uint16_t* op = a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)q * a.o_sn + hl * 4 + dt * 32;
+  if (a.nsplit <= 4) {
+    // up to four chunks: every load issued at once (indices clamped to the last chunk, whose
+    // weight is then zero), one round trip instead of two
+    constexpr int NS = 4;
+    float m4[NS], l4[NS];
+    f32x16 p4[NS];
+#pragma unroll
+    for (int c = 0; c < NS; ++c) {
+      const int cc = c < a.nsplit ? c : a.nsplit - 1;
+      const float* ml = a.part_ml + (sl0 + cc * WAVES) * 128 + lane;
+      m4[c] = ml[0];
+      l4[c] = ml[64];
+      const float* pc = a.part + (sl0 + cc * WAVES) * FRAG + dt * 16 * 64 + lane;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) p4[c][i] = pc[i * 64];
+    }
+    float mx = m4[0];
+#pragma unroll
+    for (int c = 1; c < NS; ++c) mx = fmaxf(mx, m4[c]);
+    float ls = 0.f;
+    f32x16 acc = f32x16{};
+#pragma unroll
+    for (int c = 0; c < NS; ++c) {
+      const float w = c < a.nsplit ? fast_exp2(m4[c] - mx) : 0.f;
+      ls += w * l4[c];
+      acc += w * p4[c];
+    }
+    const float iv = 1.f / ls;
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      u32x2 w = {pack2<F16>(acc[gq * 4 + 0] * iv, acc[gq * 4 + 1] * iv),
+                 pack2<F16>(acc[gq * 4 + 2] * iv, acc[gq * 4 + 3] * iv)};
+      *(u32x2*)(op + gq * 8) = w;
+    }
+    if (a.lse && dt == 0 && hl == 0) a.lse[(int64_t)bh * a.tokens + q] = (mx + __log2f(ls)) * LN2;
+    return;
+  }
   float mc[MAX_SPLIT], lc[MAX_SPLIT], mmax = -__builtin_inff();
 #pragma unroll
   for (int c = 0; c < MAX_SPLIT; ++c) {
@@ -775,8 +815,6 @@ __global__ __launch_bounds__(128 * HALVES) void merge_kernel(AttnArgs a) {
       for (int i = 0; i < 16; ++i) sum[i] += mc[c] * pc[i * 64];
     }
   }
-  const int q = gtile * QT + wave * 32 + ql;
-  uint16_t* op = a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)q * a.o_sn + hl * 4 + dt * 32;
 #pragma unroll
   for (int gq = 0; gq < 4; ++gq) {
     u32x2 w = {pack2<F16>(sum[gq * 4 + 0] * inv, sum[gq * 4 + 1] * inv),
