@@ -262,9 +262,9 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   if (tid == 0) {
     const int rank = blockIdx.x / nq;
     int i0 = item_of(qx, rank), i1 = item_of(qx, rank + dealt(qx));
-    // a queue shorter than its dealt share: claim (steal) instead
-    if (i0 < 0) i0 = claim_from(atomicAdd(&a.counters[qx], 1));
-    if (i1 < 0) i1 = claim_from(atomicAdd(&a.counters[qx], 1));
+    // a queue shorter than its dealt share: claim (steal) instead, unless every item is dealt
+    if (i0 < 0 && !all_dealt) i0 = claim_from(atomicAdd(&a.counters[qx], 1));
+    if (i1 < 0 && !all_dealt) i1 = claim_from(atomicAdd(&a.counters[qx], 1));
     s_claim[0] = i0;
     s_claim[1] = i1;
   }
