@@ -171,8 +171,14 @@ __device__ __forceinline__ u32x2 read_tr(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p));
 }
 
+// Paired workgroups (four waves, one per SIMD) per CU, i.e. waves per SIMD: two for D = 128 (64 KiB
+// of K/V stages, about 250 registers per lane), three for D = 64 (32 KiB of stages, at most 168
+// registers).  Against two, three made D = 64 calls 5-9 % faster at 2048 and 4096 px.
+template <int HALVES, int D>
+constexpr int groups_per_cu() { return HALVES == 2 && D == 64 ? 3 : 2; }
+
 template <int HALVES, int D, int KBR, bool F16>
-__global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs a) {
+__global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, D>() : 1)) void attn_fwd_kernel(AttnArgs a) {
   constexpr int WAVES = 2 * HALVES;             // waves per workgroup, 32 queries each
   constexpr int QT = 64 * HALVES;               // queries per work item
   constexpr int NG = 1;                         // 32-query groups per wave
@@ -455,9 +461,10 @@ __global__ __launch_bounds__(128 * HALVES, HALVES) void attn_fwd_kernel(AttnArgs
   // issued at the hand-over would hold up that wait and the step barrier's fence behind them.
   // The address of a lane's output row is the item's (uniform) base plus a lane offset that
   // never changes, so the pending state costs the packed values and the LSE only.  With 128-key
-  // blocks the extra registers would spill, so those tables store at the epilogue.
+  // blocks the extra registers would spill, and the D = 64 kernel keeps to 168 registers for
+  // three waves per SIMD, so those store at the epilogue.
   static_assert(NG == 1, "one pending output tile per wave");
-  constexpr bool DEFER_OUTPUT = KBR == 1;
+  constexpr bool DEFER_OUTPUT = KBR == 1 && groups_per_cu<HALVES, D>() == 2;
   const int o_lane = (wave * QW + ql) * a.o_sn + hl * 8;
   const int l_lane = wave * QW + ql;
   u32x2 ow[DT][4];
@@ -960,7 +967,11 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, float*
   a.part = (float*)((char*)workspace + p.counters_bytes);
   a.part_ml = (float*)((char*)workspace + p.counters_bytes + p.part_bytes);
   const int64_t items = (int64_t)a.bh * p.per_bh;
-  int groups = num_groups > 0 ? num_groups : 2 * device_cu_count();
+  // three workgroups per CU where the kernel fits them, once there are enough items to keep
+  // them busy (small problems finish sooner on two, whose items run faster)
+  const int cus = device_cu_count();
+  const int per_cu = paired && head_dim == 64 && items >= 8 * 3 * (int64_t)cus ? groups_per_cu<2, 64>() : 2;
+  int groups = num_groups > 0 ? num_groups : per_cu * cus;
   if (groups > items) groups = (int)items;
   if (groups < 1) return HB_OK;
   if (clear_counters) {
