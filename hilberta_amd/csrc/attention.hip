@@ -967,10 +967,10 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, float*
   a.part = (float*)((char*)workspace + p.counters_bytes);
   a.part_ml = (float*)((char*)workspace + p.counters_bytes + p.part_bytes);
   const int64_t items = (int64_t)a.bh * p.per_bh;
-  // three workgroups per CU where the kernel fits them, once there are enough items to keep
-  // them busy (small problems finish sooner on two, whose items run faster)
+  // three workgroups per CU where the kernel fits them, once each gets two items or more (with
+  // fewer, the call finishes sooner on two workgroups per CU, whose items run faster)
   const int cus = device_cu_count();
-  const int per_cu = paired && head_dim == 64 && items >= 8 * 3 * (int64_t)cus ? groups_per_cu<2, 64>() : 2;
+  const int per_cu = paired && head_dim == 64 && items >= 2 * 3 * (int64_t)cus ? groups_per_cu<2, 64>() : 2;
   int groups = num_groups > 0 ? num_groups : per_cu * cus;
   if (groups > items) groups = (int)items;
   if (groups < 1) return HB_OK;

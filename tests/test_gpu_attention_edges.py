@@ -1,6 +1,7 @@
 """GPU edge cases of the attention path: table padding, the C ABI's all_queries=0 mode, 4096 px
-(sampled rows, and every row of all four phases), B=2 with BNHD views and 128-key tables at
-2048 px, and the permutation at 4096 px sizes.
+(sampled rows, and every row of all four phases), D = 64 at 2048 px (every row; the D = 64 kernel
+runs three workgroups per CU there), B=2 with BNHD views and 128-key tables at 2048 px, and the
+permutation at 4096 px sizes.
 
 References are the fp32 oracle formulations in oracle/attention.py (block form on sampled query
 tiles, computed on the device in fp32), the kernel's own all_queries=1 output (bitwise), and
@@ -125,12 +126,13 @@ def _block_reference_all_heads(qd, kd, vd, plan, phase):
     heads, which at 4096 px means 24k small launches per phase)."""
     G = plan["global_tokens"]
     p = plan["phases"][phase]
+    scale = qd.shape[-1] ** -0.5
     qf, kf, vf = qd.float(), kd.float(), vd.float()
     ref_o = torch.empty_like(qf)
     ref_l = torch.empty(qf.shape[:3], dtype=torch.float32, device=qf.device)
     for h0 in range(0, qf.shape[1], 6):
         hs = slice(h0, h0 + 6)
-        s = torch.matmul(qf[:, hs, :G], kf[:, hs].transpose(-1, -2).contiguous()) * D**-0.5
+        s = torch.matmul(qf[:, hs, :G], kf[:, hs].transpose(-1, -2).contiguous()) * scale
         ref_l[:, hs, :G] = torch.logsumexp(s, -1)
         ref_o[:, hs, :G] = torch.matmul(torch.softmax(s, -1), vf[:, hs])
         del s
@@ -139,7 +141,7 @@ def _block_reference_all_heads(qd, kd, vd, plan, phase):
         q0 = G + 64 * row
         cols = (ids_all[row, :count, None] * 64 + torch.arange(64, device=qd.device)).reshape(-1)
         s = torch.matmul(qf[:, :, q0 : q0 + 64], kf[:, :, cols].transpose(-1, -2).contiguous())
-        s = s * D**-0.5
+        s = s * scale
         ref_l[:, :, q0 : q0 + 64] = torch.logsumexp(s, -1)
         ref_o[:, :, q0 : q0 + 64] = torch.matmul(torch.softmax(s, -1), vf[:, :, cols])
     return ref_o, ref_l
@@ -164,6 +166,26 @@ def test_paired_4096_full_output(hip_device, phase):
     torch.cuda.synchronize()
     ref_o, ref_l = _block_reference_all_heads(q, k, v, plan, phase)
     compare(out, lse, ref_o, ref_l, f"4096_t16k3 phase {phase} all rows")
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_paired_2048_head_dim_64_full_output(hip_device, f16):
+    """D = 64 at 2048 px 16-tile K3, 24 heads (3360 items: the D = 64 kernel then runs three
+    workgroups per CU): every query row, output and LSE, against the block formulation."""
+    from hilberta_amd.paired_kernel import paired_attention
+
+    _QKV_4096.clear()
+    plan = oracle_plan("2048_t16k3")
+    N = plan["total_tokens"]
+    dtype = torch.float16 if f16 else torch.bfloat16
+    q, k, v = (x.to(hip_device) for x in A.seeded_qkv(1, 24, N, 64, seed=11, dtype=dtype))
+    say(f"case paired 2048_t16k3 D=64 {'fp16' if f16 else 'bf16'} phase 2 full output")
+    meta = device_paired(oracle_paired(plan, 2), hip_device)
+    lse = torch.empty(1, 24, N, dtype=torch.float32, device=hip_device)
+    out = paired_attention(q, k, v, meta, lse=lse)
+    torch.cuda.synchronize()
+    ref_o, ref_l = _block_reference_all_heads(q, k, v, plan, 2)
+    compare(out, lse, ref_o, ref_l, f"2048_t16k3 D=64 {'fp16' if f16 else 'bf16'} all rows")
 
 
 def test_paired_2048_batch2_bnhd_key_block_128(hip_device):
