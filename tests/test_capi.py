@@ -79,6 +79,8 @@ def test_global_tile_split_plan():
     assert _global_chunks(1, 24, 4608, 512, 72) == 1
     # 4096 px 16-tile K3 (1032 key blocks, width 75): two chunks of 516
     assert _global_chunks(1, 24, 66048, 512, 75) == 2
+    # one head of it: fourteen chunks of 74 (merge_kernel's general path, past four chunks)
+    assert _global_chunks(1, 1, 66048, 512, 75) == 14
 
 
 def test_pair_rows_rejections():

@@ -117,6 +117,30 @@ def test_paired_4096_sampled_rows(hip_device):
     _sampled_rows_check(out, lse, q, k, v, plan, phase, rows, "4096")
 
 
+def test_paired_4096_one_head_many_chunks(hip_device):
+    """One head at 4096 px: the planner splits each global tile into 14 chunks (more than the
+    merge kernel's four-chunk fast path takes, tests/test_capi.py), so the general merge runs;
+    global rows against fp32 attention over all keys, and sampled ordinary rows."""
+    from hilberta_amd.paired_kernel import paired_attention
+
+    plan = oracle_plan("4096_t16k3")
+    N, G = plan["total_tokens"], plan["global_tokens"]
+    q, k, v = (x.to(hip_device) for x in A.seeded_qkv(1, 1, N, D, seed=12))
+    phase = 3
+    meta = device_paired(oracle_paired(plan, phase), hip_device)
+    lse = torch.empty(1, 1, N, dtype=torch.float32, device=hip_device)
+    say("case paired 4096_t16k3 one head, global tiles in 14 chunks")
+    out = paired_attention(q, k, v, meta, lse=lse)
+    torch.cuda.synchronize()
+    qf, kf, vf = q.float(), k.float(), v.float()
+    s = torch.matmul(qf[:, :, :G], kf.transpose(-1, -2).contiguous()) * D**-0.5
+    compare(out[:, :, :G], lse[:, :, :G], torch.matmul(torch.softmax(s, -1), vf),
+            torch.logsumexp(s, -1), "4096 one head global rows")
+    nq = len(plan["phases"][phase]["kv_counts"])
+    rows = sorted(set(np.random.default_rng(5).choice(nq, 8, replace=False).tolist()) | {0, nq - 1})
+    _sampled_rows_check(out, lse, q, k, v, plan, phase, rows, "4096 one head")
+
+
 _QKV_4096: dict = {}
 
 
