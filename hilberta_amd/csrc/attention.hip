@@ -9,9 +9,10 @@
 //    than the longest ordinary row or MIN_CHUNK steps, so no item dominates the schedule; chunk
 //    partials (unnormalised accumulator, running max, row sum) go to the workspace and
 //    merge_kernel combines them after the main kernel.
-//  * Persistent workgroups (2 per CU) claim items from 8 work queues, one per XCD (queue x =
-//    blockIdx % 8, the XCD under round-robin dispatch, owns a contiguous range of the item list),
-//    so items that share K/V blocks run under one L2; idle workgroups steal from other queues.
+//  * Persistent workgroups (2 per CU; 3 for paired D = 64 calls with enough items) claim items
+//    from 8 work queues, one per XCD (queue x = blockIdx % 8, the XCD under round-robin dispatch,
+//    owns a contiguous range of the item list), so items that share K/V blocks run under one L2;
+//    idle workgroups steal from other queues, skipping those a drained-queue mask marks empty.
 //    Each workgroup's first two items are dealt out without atomics; later claims run one item
 //    ahead, and the next item's table entries, first K/V block and Q tile are prefetched while
 //    the current item finishes.
