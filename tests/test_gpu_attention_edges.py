@@ -1,7 +1,7 @@
 """GPU edge cases of the attention path: table padding, the C ABI's all_queries=0 mode, 4096 px
-(sampled rows, and every row of all four phases), D = 64 at 2048 px (every row; the D = 64 kernel
-runs three workgroups per CU there), B=2 with BNHD views and 128-key tables at 2048 px, and the
-permutation at 4096 px sizes.
+(sampled rows, and every row of all four phases), D = 64 and the adapter's BNHD storage at
+2048 px (every row; the D = 64 kernel runs three workgroups per CU there), B=2 with BNHD views and
+128-key tables at 2048 px, and the permutation at 4096 px sizes.
 
 References are the fp32 oracle formulations in oracle/attention.py (block form on sampled query
 tiles, computed on the device in fp32), the kernel's own all_queries=1 output (bitwise), and
@@ -190,6 +190,28 @@ def test_paired_4096_full_output(hip_device, phase):
     torch.cuda.synchronize()
     ref_o, ref_l = _block_reference_all_heads(q, k, v, plan, phase)
     compare(out, lse, ref_o, ref_l, f"4096_t16k3 phase {phase} all rows")
+
+
+def test_paired_2048_adapter_layout_full_output(hip_device):
+    """The adapter's storage (flux_adapter.py:280-326): Q/K/V projected as [B, N, H, D] and
+    viewed as [B, H, N, D] (strides N*H*D, D, H*D, 1), 2048 px 16-tile K3, 24 heads: every row of
+    one phase, output (in the same storage order) and LSE, against the block formulation."""
+    from hilberta_amd.paired_kernel import paired_attention
+
+    _QKV_4096.clear()
+    plan = oracle_plan("2048_t16k3")
+    N = plan["total_tokens"]
+    q, k, v = A.seeded_qkv(1, 24, N, D, seed=13)
+    qd, kd, vd = (x.transpose(1, 2).contiguous().to(hip_device).transpose(1, 2) for x in (q, k, v))
+    assert qd.stride() == (N * 24 * D, D, 24 * D, 1)
+    say("case paired 2048_t16k3 BNHD views phase 1 full output")
+    meta = device_paired(oracle_paired(plan, 1), hip_device)
+    lse = torch.empty(1, 24, N, dtype=torch.float32, device=hip_device)
+    out = paired_attention(qd, kd, vd, meta, lse=lse)
+    torch.cuda.synchronize()
+    assert out.stride() == qd.stride()
+    ref_o, ref_l = _block_reference_all_heads(qd, kd, vd, plan, 1)
+    compare(out, lse, ref_o, ref_l, "2048_t16k3 BNHD views all rows")
 
 
 @pytest.mark.parametrize("f16", [False, True])
