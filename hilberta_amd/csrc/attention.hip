@@ -268,7 +268,10 @@ __global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, 
     return -1;
   };
   if (tid == 0) {
-    const int rank = blockIdx.x / nq;
+    // ranks rotated by half: the first items of a queue (its global chunks, the longest) go to
+    // the upper half of the grid, which issues at the higher priority (0.3-3 % faster, most at
+    // 1024 px 16-tile K3; bitwise identical)
+    const int rank = ((int)blockIdx.x / nq + dealt(qx) / 2) % dealt(qx);
     int i0 = item_of(qx, rank), i1 = item_of(qx, rank + dealt(qx));
     // a queue shorter than its dealt share: claim (steal) instead, unless every item is dealt
     if (i0 < 0 && !all_dealt) i0 = claim_from(atomicAdd(&a.counters[qx], 1));
