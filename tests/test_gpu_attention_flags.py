@@ -52,7 +52,7 @@ def few_groups(monkeypatch):
 
 
 @pytest.mark.parametrize("key_block_size", [64, 128])
-@pytest.mark.parametrize("groups", [8, 3, 0])
+@pytest.mark.parametrize("groups", [8, 3, 1, 0])
 def test_paired_zero_global_prefix(hip_device, few_groups, key_block_size, groups):
     """G = 0: every paired row's first union entry has its own flags (1, 2 or 3)."""
     from hilberta_amd.paired_kernel import paired_attention
