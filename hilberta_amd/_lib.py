@@ -35,6 +35,11 @@ SIGNATURES = {
         [_p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _c_int,
          _c_int, _c_int, _c_f32, _c_int, _p],
     ),
+    "hb_quad_fwd": (
+        _c_int,
+        [_p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _c_int,
+         _c_int, _c_f32, _p, _c_i64, _c_int, _p],
+    ),
     "hb_block_sparse_fwd": (
         _c_int,
         [_p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p, _c_int, _c_int,
@@ -64,6 +69,7 @@ SIGNATURES = {
     "hb_bits_counts": (_c_int, [_p, _c_int, _c_int, _c_int, _p, _p, _p, _p]),
     "hb_bits_emit": (_c_int, [_p, _c_int, _c_int, _c_int, _p, _c_int, _p, _p, _c_int, _p]),
     "hb_pair_rows": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _p, _p]),
+    "hb_quad_rows": (_c_int, [_p, _p, _p, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _p, _p]),
 }
 
 _lib = None
@@ -73,6 +79,14 @@ def header_symbols() -> list[str]:
     """Function names declared in include/hilberta_hip.h."""
     text = HEADER.read_text()
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(hb_\w+)\s*\(", text, re.M)))
+
+
+def header_abi_version() -> int:
+    """HB_ABI_VERSION as include/hilberta_hip.h defines it."""
+    m = re.search(r"^#define\s+HB_ABI_VERSION\s+(\d+)", HEADER.read_text(), re.M)
+    if not m:
+        raise RuntimeError(f"{HEADER} defines no HB_ABI_VERSION")
+    return int(m.group(1))
 
 
 def load():
@@ -85,6 +99,13 @@ def load():
                 "there is no CPU fallback"
             )
         lib = ctypes.CDLL(str(LIB_PATH))
+        lib.hb_version.restype = ctypes.c_int32
+        built, declared = lib.hb_version(), header_abi_version()
+        if built != declared:
+            raise RuntimeError(
+                f"{LIB_PATH} was built for ABI {built} but include/hilberta_hip.h declares ABI "
+                f"{declared}: rebuild the HIP library (python -m hilberta_amd.build)"
+            )
         for name, (restype, argtypes) in SIGNATURES.items():
             fn = getattr(lib, name, None)
             if fn is None:

@@ -3,13 +3,15 @@
 // Replaces the Triton kernels _paired_fwd (reference hilberta/paired_kernel.py:18-94) and
 // _block_sparse_fwd (hilberta/sparse_kernel.py:28-97) with one hand-written CDNA4 kernel:
 //
-//  * Work item = one query tile (128 queries for paired tables, 64 for unpaired ones) of one
-//    (batch, head), or one chunk of a global (text) query tile's all-key sweep.  Global tiles are
+//  * Work item = one query tile (256 queries for quad tables, 128 for paired tables, 64 for
+//    unpaired ones) of one (batch, head), or one chunk of a global (text) query tile's all-key
+//    sweep.  Global tiles are
 //    split into at most MAX_SPLIT chunks of about half a workgroup's average work, none shorter
 //    than the longest ordinary row or MIN_CHUNK steps, so no item dominates the schedule; chunk
 //    partials (unnormalised accumulator, running max, row sum) go to the workspace and
 //    merge_kernel combines them after the main kernel.
-//  * Persistent workgroups (2 per CU; 3 for paired D = 64 calls with enough items) claim items
+//  * Persistent workgroups (2 per CU; 3 for paired D = 64 calls with enough items; 1 eight-wave
+//    workgroup per CU for quad tables) claim items
 //    from 8 work queues, one per XCD (queue x = blockIdx % 8, the XCD under round-robin dispatch,
 //    owns a contiguous range of the item list), so items that share K/V blocks run under one L2;
 //    idle workgroups steal from other queues, skipping those a drained-queue mask marks empty.
@@ -25,7 +27,10 @@
 //    cross-half exchange (v_permlane32_swap), and the output O^T = V^T P^T takes the score
 //    registers directly as the B operand; its A operand (V^T) comes out of LDS already
 //    transposed through ds_read_b64_tr_b16.
-//  * Each wave owns 32 queries; in paired mode waves 0-1 own query half 0 and waves 2-3 half 1.
+//  * Each wave owns 32 queries; in paired mode waves 0-1 own query half 0 and waves 2-3 half 1;
+//    with quad tables (two paired rows merged, flag bit = 64-query block 0..3) waves 2b and
+//    2b + 1 own query block b, and the eight waves share each staged K/V tile, so a tile costs
+//    half the load instructions and LDS writes per MFMA of a paired item.
 //    A block that the flag test (flags >> (half + 2*key_half)) & 1 of paired_kernel.py:65,83-84
 //    hides from a wave's half is computed but masked (P = 0), which keeps one code path (a
 //    wave-uniform branch around the masked case measured slower: the compiler's schedule of the
@@ -175,11 +180,13 @@ __device__ __forceinline__ u32x2 read_tr(const uint16_t* p) {
 // Paired workgroups (four waves, one per SIMD) per CU, i.e. waves per SIMD: two for D = 128 (64 KiB
 // of K/V stages, about 250 registers per lane), three for D = 64 (32 KiB of stages, at most 168
 // registers).  Against two, three made D = 64 calls 5-9 % faster at 2048 and 4096 px.
+//  Quad workgroups (eight waves) fill a CU alone at two waves per SIMD.
 template <int HALVES, int D>
-constexpr int groups_per_cu() { return HALVES == 2 && D == 64 ? 3 : 2; }
+constexpr int groups_per_cu() { return HALVES == 4 ? 1 : (HALVES == 2 && D == 64 ? 3 : 2); }
 
 template <int HALVES, int D, int KBR, bool F16>
 __global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, D>() : 1)) void attn_fwd_kernel(AttnArgs a) {
+  static_assert(HALVES == 1 || HALVES == 2 || (HALVES == 4 && KBR == 1), "quad tables use 64-key blocks");
   constexpr int WAVES = 2 * HALVES;             // waves per workgroup, 32 queries each
   constexpr int QT = 64 * HALVES;               // queries per work item
   constexpr int NG = 1;                         // 32-query groups per wave
@@ -200,16 +207,21 @@ __global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  // The upper half of the persistent grid issues at a higher wave priority.  Two workgroups share
-  // each CU, and with equal priorities their waves tend to reach the MFMA and softmax phases
-  // together; the asymmetry lets one run ahead (5-7 % faster at 2048 px 16-tile K3, measured
-  // against the symmetric kernel in one process; neutral on dense tables).  A workgroup whose
-  // claim finds every queue drained gives the priority up for its last item (see `step`).
-  if (blockIdx.x >= gridDim.x / 2) __builtin_amdgcn_s_setprio(1);
   // wave index as a provably uniform (scalar) value, so per-wave tests such as the flag check
   // compile to branches rather than exec-masked code
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = HALVES == 2 ? (wave * QW) / 64 : 0;
+  // Two waves share each SIMD, and with equal priorities they tend to reach the MFMA and softmax
+  // phases together; a higher issue priority for one of them lets it run ahead.  With two
+  // workgroups per CU the upper half of the persistent grid takes it (5-7 % faster at 2048 px
+  // 16-tile K3, measured against the symmetric kernel in one process; neutral on dense tables),
+  // and a workgroup whose claim finds every queue drained gives it up for its last item (see
+  // `step`).  An eight-wave quad workgroup holds both waves of each SIMD (waves w and w + 4
+  // under round-robin placement): its upper four waves take it.
+  if (HALVES == 4 ? wave >= 4 : blockIdx.x >= gridDim.x / 2) __builtin_amdgcn_s_setprio(1);
+  // query block (64 queries) of this wave: the flag bit it tests
+  const int half = HALVES >= 2 ? (wave * QW) / 64 : 0;
+  // flags of a block every query block of the item sees (global chunks)
+  constexpr int ALL_FLAGS = HALVES == 4 ? 15 : 3;
   const int ql = lane & 31;   // query (column) owned by this lane inside the wave's 32
   const int hl = lane >> 5;   // lane half: selects the 8-element k slice of MFMA operands
 
@@ -321,7 +333,7 @@ __global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, 
     const int64_t row = (int64_t)it.row * a.width;
     cnt = a.counts[it.row];
     t_id = row_entry(a.indices + row, a.width, lane);
-    if (HALVES == 2) t_fl = row_entry(a.flags + row, a.width, lane);
+    if (HALVES >= 2) t_fl = row_entry(a.flags + row, a.width, lane);
   };
 
   Item cur = decode(uniform(s_claim[0]));
@@ -340,7 +352,7 @@ __global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, 
   auto step_info = [&](int s, int& kb, int& fl) {
     if (cur.global) {
       kb = cur.first_block + s;
-      fl = 3;
+      fl = ALL_FLAGS;
       return;
     }
     const int e = s / KBR;
@@ -349,13 +361,14 @@ __global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, 
       tbase = e & ~63;
       const int64_t row = (int64_t)cur.row * a.width;
       t_id = row_entry(a.indices + row, a.width, tbase + lane);
-      t_fl = HALVES == 2 ? row_entry(a.flags + row, a.width, tbase + lane) : 0;
+      t_fl = HALVES >= 2 ? row_entry(a.flags + row, a.width, tbase + lane) : 0;
       // Wait here, inside the refill branch, for the entries read just below: left pending past
       // the branch, the waitcnt pass would stall the next LDS reads on every path (vmcnt(0)).
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
     kb = __builtin_amdgcn_readlane(t_id, e - tbase) * KBR + sub;
-    fl = HALVES == 2 ? (__builtin_amdgcn_readlane(t_fl, e - tbase) >> (2 * sub)) & 3 : 1;
+    if constexpr (HALVES == 4) fl = __builtin_amdgcn_readlane(t_fl, e - tbase) & 15;
+    else fl = HALVES == 2 ? (__builtin_amdgcn_readlane(t_fl, e - tbase) >> (2 * sub)) & 3 : 1;
   };
   // First step at or after s that some query half may see.  With one step per table entry every
   // entry qualifies (paired entries carry at least one flag bit), so only 128-key blocks (two
@@ -469,7 +482,7 @@ __global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, 
   // blocks the extra registers would spill, and the D = 64 kernel keeps to 168 registers for
   // three waves per SIMD, so those store at the epilogue.
   static_assert(NG == 1, "one pending output tile per wave");
-  constexpr bool DEFER_OUTPUT = KBR == 1 && groups_per_cu<HALVES, D>() == 2;
+  constexpr bool DEFER_OUTPUT = KBR == 1 && (HALVES == 4 || groups_per_cu<HALVES, D>() == 2);
   const int o_lane = (wave * QW + ql) * a.o_sn + hl * 8;
   const int l_lane = wave * QW + ql;
   u32x2 ow[DT][4];
@@ -572,7 +585,8 @@ __global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, 
       // so a workgroup of the same CU still running its own last items is not held back by it
       // (4 % faster at 1024 px, where every item is dealt out and the second is the last, 1.5-2 %
       // on dense tables, 0.5-1.3 % at 2048 px 16-tile K3; bitwise identical).
-      if (nxt_idx < 0) __builtin_amdgcn_s_setprio(0);
+      // (A quad workgroup has the CU to itself and keeps its waves' asymmetry.)
+      if (HALVES != 4 && nxt_idx < 0) __builtin_amdgcn_s_setprio(0);
       if (!meta_late) load_meta(decode(nxt_idx), n_cnt, n_id, n_fl);
     }
     if (!cross) {
@@ -584,7 +598,8 @@ __global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, 
       // with an entry only one half sees), sub-step 0 of it for 128-key blocks
       const Item nxt = decode(nxt_idx);
       c_kb = nxt.global ? nxt.first_block : __builtin_amdgcn_readlane(n_id, 0) * KBR;
-      c_fl = nxt.global ? 3 : (HALVES == 2 ? __builtin_amdgcn_readlane(n_fl, 0) & 3 : 1);
+      c_fl = nxt.global ? ALL_FLAGS
+                        : (HALVES >= 2 ? __builtin_amdgcn_readlane(n_fl, 0) & ALL_FLAGS : 1);
       dma_block(other, k_base(nxt), v_base(nxt), c_kb);
     }
     flush_output();  // the previous item's output, behind this step's loads
@@ -847,13 +862,17 @@ struct Plan {
   int64_t counters_bytes, part_bytes, ml_bytes;
 };
 
+// paired: 0 = unpaired 64-query rows, 1 = paired 128-query rows, 2 = quad 256-query rows
 int make_plan(Plan& p, int batch, int heads, int tokens, int head_dim, int global_tokens, int width,
               int key_block_size, int paired, int all_queries) {
   HB_REQUIRE(batch > 0 && heads > 0 && tokens > 0, "batch, heads and tokens must be positive");
   HB_REQUIRE(head_dim == 64 || head_dim == 128, "head_dim must be 64 or 128 (got %d)", head_dim);
   // (a table row is read through a buffer whose byte size is a 32-bit width * 4)
   HB_REQUIRE(width >= 1 && width < (1 << 28), "table width must be in [1, 2^28) (got %d)", width);
-  p.halves = paired ? 2 : 1;
+  HB_REQUIRE(paired >= 0 && paired <= 2, "table kind must be 0 (unpaired), 1 (paired) or 2 (quad)");
+  HB_REQUIRE(paired != 2 || (head_dim == 128 && key_block_size == 64),
+             "quad tables take head_dim 128 and 64-key blocks");
+  p.halves = paired == 2 ? 4 : (paired ? 2 : 1);
   p.qt = 64 * p.halves;
   p.waves = 2 * p.halves;
   p.d = head_dim;
@@ -876,7 +895,9 @@ int make_plan(Plan& p, int batch, int heads, int tokens, int head_dim, int globa
   const int64_t row_steps = (int64_t)width * p.kbr;
   const int64_t all_steps =
       (int64_t)batch * heads * ((int64_t)p.rows * row_steps + (int64_t)p.global_tiles * p.key_blocks);
-  int64_t target = ((all_steps + NOMINAL_GROUPS - 1) / NOMINAL_GROUPS + 1) / 2;
+  // (quad workgroups are half as many, one per CU)
+  const int64_t nominal = p.halves == 4 ? NOMINAL_GROUPS / 2 : NOMINAL_GROUPS;
+  int64_t target = ((all_steps + nominal - 1) / nominal + 1) / 2;
   if (target < row_steps) target = row_steps;
   if (target < MIN_CHUNK) target = MIN_CHUNK;
   int nsplit = (int)((p.key_blocks + target - 1) / target);
@@ -943,6 +964,9 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, float*
   for (int i = 0; i < 12; ++i)
     HB_REQUIRE(strides[i] > 0 && strides[i] % 8 == 0 && strides[i] < (1ll << 31),
                "Q/K/V/out outer strides must be positive multiples of 8 elements below 2^31");
+  // a lane's output row inside an item is addressed with a 32-bit element offset
+  HB_REQUIRE((int64_t)p.qt * strides[11] + head_dim < (1ll << 31),
+             "output token stride too large: %d rows must span fewer than 2^31 elements", p.qt);
   // K/V blocks are addressed with 32-bit byte offsets from each (batch, head) base
   HB_REQUIRE(((int64_t)tokens * (strides[5] > strides[8] ? strides[5] : strides[8])) * 2 < (1ll << 31),
              "K/V token stride too large: one (batch, head) must span less than 2 GiB");
@@ -980,7 +1004,8 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, float*
   // three workgroups per CU where the kernel fits them, once each gets two items or more (with
   // fewer, the call finishes sooner on two workgroups per CU, whose items run faster)
   const int cus = device_cu_count();
-  const int per_cu = paired && head_dim == 64 && items >= 2 * 3 * (int64_t)cus ? groups_per_cu<2, 64>() : 2;
+  const int per_cu = p.halves == 4 ? groups_per_cu<4, 128>()
+                     : paired && head_dim == 64 && items >= 2 * 3 * (int64_t)cus ? groups_per_cu<2, 64>() : 2;
   int groups = num_groups > 0 ? num_groups : per_cu * cus;
   if (groups > items) groups = (int)items;
   if (groups < 1) return HB_OK;
@@ -988,7 +1013,10 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, float*
     static_assert(QUEUES + 2 <= 64, "the counters fit the cleared 256 bytes");
     hipLaunchKernelGGL(clear_counters_kernel, dim3(1), dim3(64), 0, stream, a.counters);
   }
-  if (paired) {
+  if (p.halves == 4) {
+    if (dtype == HB_DTYPE_F16) launch<4, 128, 1, true>(a, groups, stream);
+    else launch<4, 128, 1, false>(a, groups, stream);
+  } else if (paired) {
     if (p.kbr == 2) dispatch_d<2, 2>(a, head_dim, dtype == HB_DTYPE_F16, groups, stream);
     else dispatch_d<2, 1>(a, head_dim, dtype == HB_DTYPE_F16, groups, stream);
   } else {
@@ -1055,6 +1083,18 @@ extern "C" int hb_paired_fwd(const void* q, const void* k, const void* v, void* 
                            kv_indices, kv_flags, kv_counts, table_width, global_tokens,
                            key_block_size, 1, all_queries, scale_log2, workspace, workspace_bytes,
                            num_groups, stream);
+}
+
+extern "C" int hb_quad_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
+                           const int64_t* strides, int32_t batch, int32_t heads, int32_t tokens,
+                           int32_t head_dim, int32_t dtype, const int32_t* kv_indices,
+                           const int32_t* kv_flags, const int32_t* kv_counts, int32_t table_width,
+                           int32_t global_tokens, int32_t all_queries, float scale_log2,
+                           void* workspace, int64_t workspace_bytes, int32_t num_groups,
+                           hipStream_t stream) {
+  return hb::attention_fwd(q, k, v, out, lse, strides, batch, heads, tokens, head_dim, dtype,
+                           kv_indices, kv_flags, kv_counts, table_width, global_tokens, 64, 2,
+                           all_queries, scale_log2, workspace, workspace_bytes, num_groups, stream);
 }
 
 extern "C" int hb_block_sparse_fwd(const void* q, const void* k, const void* v, void* out,

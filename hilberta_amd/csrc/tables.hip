@@ -562,3 +562,83 @@ extern "C" int hb_pair_rows(const int32_t* kv_indices, const int32_t* kv_counts,
   HB_HIP(hipGetLastError());
   return HB_OK;
 }
+
+// Quad rows for the 256-query attention items: one wave per quad row r merges the rows of r's
+// group (group 2: paired rows 2r, 2r + 1 with 64-key flags bit half; group 4: unpaired rows
+// 4r .. 4r + 3) into a per-key-block flag byte in LDS, bit b set where 64-query block b of the
+// quad row (b = 2 * paired row + half, or the unpaired row) sees the key block, then writes the
+// union in ascending key-block order, zero padded to out_width, with its count.  The same union
+// as pair_metadata (paired_metadata.py:38-51) taken over four query blocks instead of two.  Ids
+// outside [0, T) and entries past a row's count (clamped to width) are ignored; a union longer
+// than out_width is cut to out_width entries and sets *overflow (when given) to 1.
+constexpr int QUAD_WORDS = PAIR_MAX_BLOCKS / 4;  // four flag bytes per word
+__global__ __launch_bounds__(TPB) void quad_rows_kernel(const int32_t* ids, const int32_t* flags,
+                                                        const int32_t* counts, int qrows, int width,
+                                                        int T, int group, int out_width,
+                                                        int32_t* out_ids, int32_t* out_flags,
+                                                        int32_t* out_counts, int32_t* overflow) {
+  __shared__ uint32_t fm[TPB / 64][QUAD_WORDS];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int qr = blockIdx.x * (TPB / 64) + w;
+  for (int i = lane; i < QUAD_WORDS; i += 64) fm[w][i] = 0u;
+  __syncthreads();
+  if (qr < qrows) {
+    const int bits = 4 / group;  // flag bits each input row contributes
+    for (int j = 0; j < group; ++j) {
+      const int row = group * qr + j;
+      const int c = min(max(counts[row], 0), width);
+      const int32_t* rid = ids + (int64_t)row * width;
+      const int32_t* rfl = flags ? flags + (int64_t)row * width : nullptr;
+      for (int e = lane; e < c; e += 64) {
+        const int p = rid[e];
+        if (p < 0 || p >= T) continue;
+        const uint32_t f = rfl ? (uint32_t)(rfl[e] & 3) : 1u;
+        atomicOr(&fm[w][p >> 2], (f << (bits * j)) << (8 * (p & 3)));
+      }
+    }
+  }
+  __syncthreads();
+  if (qr >= qrows) return;
+  int32_t* oid = out_ids + (int64_t)qr * out_width;
+  int32_t* ofl = out_flags + (int64_t)qr * out_width;
+  int base = 0;
+  for (int kb0 = 0; kb0 < T; kb0 += 64) {
+    const int kb = kb0 + lane;
+    const int flag = kb < T ? (int)((fm[w][kb >> 2] >> (8 * (kb & 3))) & 15u) : 0;
+    const uint64_t live = __ballot(flag != 0);
+    const int pos = base + __popcll(live & ((1ull << lane) - 1));
+    if (flag && pos < out_width) {
+      oid[pos] = kb;
+      ofl[pos] = flag;
+    }
+    base += __popcll(live);
+  }
+  const int cnt = min(base, out_width);
+  for (int e = cnt + lane; e < out_width; e += 64) {
+    oid[e] = 0;
+    ofl[e] = 0;
+  }
+  if (lane == 0) out_counts[qr] = cnt;
+  if (lane == 0 && base > out_width && overflow) atomicOr(overflow, 1);
+}
+
+extern "C" int hb_quad_rows(const int32_t* kv_indices, const int32_t* kv_flags,
+                            const int32_t* kv_counts, int32_t rows, int32_t width,
+                            int32_t total_blocks, int32_t* quad_ids, int32_t* quad_flags,
+                            int32_t* quad_counts, int32_t quad_width, int32_t* overflow,
+                            hb_stream_t stream) {
+  HB_REQUIRE(kv_indices && kv_counts && quad_ids && quad_flags && quad_counts,
+             "null pointer argument");
+  const int group = kv_flags ? 2 : 4;
+  HB_REQUIRE(rows > 0 && rows % group == 0,
+             "rows must be a positive multiple of %d (got %d)", group, rows);
+  HB_REQUIRE(width > 0 && quad_width > 0, "table widths must be positive");
+  HB_REQUIRE(total_blocks > 0 && total_blocks <= PAIR_MAX_BLOCKS,
+             "total_blocks must be in [1, %d] (got %d)", PAIR_MAX_BLOCKS, total_blocks);
+  const int qrows = rows / group, per_block = TPB / 64;
+  hipLaunchKernelGGL(quad_rows_kernel, dim3((qrows + per_block - 1) / per_block), dim3(TPB), 0,
+                     stream, kv_indices, kv_flags, kv_counts, qrows, width, total_blocks, group,
+                     quad_width, quad_ids, quad_flags, quad_counts, overflow);
+  HB_HIP(hipGetLastError());
+  return HB_OK;
+}

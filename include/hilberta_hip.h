@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define HB_ABI_VERSION 2
+#define HB_ABI_VERSION 3
 #define HB_DTYPE_BF16 0
 #define HB_DTYPE_F16 1
 
@@ -36,7 +36,8 @@ int hb_stream_capture_id(hb_stream_t stream, uint64_t* capture_id);
  * the shapes are rejected).  It holds the work-queue counters (first 256 bytes) and the partial
  * results of split global query tiles.  It must be zero-filled once before first use; every
  * launch leaves the counters at zero again, so one workspace serves all later launches.
- * Launches that overlap in time must not share a workspace.
+ * Launches that overlap in time must not share a workspace.  paired: 0 = unpaired tables
+ * (hb_block_sparse_fwd), 1 = paired (hb_paired_fwd), 2 = quad (hb_quad_fwd).
  */
 int64_t hb_attention_workspace_bytes(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
                                      int32_t global_tokens, int32_t table_width,
@@ -62,6 +63,24 @@ int hb_paired_fwd(const void* q, const void* k, const void* v, void* out, float*
                   int32_t global_tokens, int32_t key_block_size, int32_t all_queries,
                   float scale_log2, void* workspace, int64_t workspace_bytes, int32_t num_groups,
                   hb_stream_t stream);
+
+/* Quad-table forward: the same launch as hb_paired_fwd (replacing the same reference launch,
+ * hilberta/paired_kernel.py:181-204, kernel :18-94) over quad tables, in which paired rows 2r
+ * and 2r + 1 are merged into one 256-query row r (hb_quad_rows): kv_indices, kv_flags int32
+ * [(N-G)/256, table_width], kv_counts int32 [(N-G)/256], flag bit b (0..3) set where 64-query
+ * block b of the row sees the 64-key block.  One eight-wave workgroup per compute unit stages
+ * each K/V block once for all 256 queries.  head_dim 128 only; N and G multiples of 256.  Every
+ * query sees the same key blocks in the same order with the same arithmetic as under
+ * hb_paired_fwd (blocks another query block needs are computed and masked to exact zeros), so
+ * ordinary rows are bitwise equal to hb_paired_fwd's; global rows may split into chunks at other
+ * places.  num_groups 0 = one per compute unit.  Workspace: hb_attention_workspace_bytes with
+ * paired = 2. */
+int hb_quad_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
+                const int64_t* strides, int32_t batch, int32_t heads, int32_t tokens,
+                int32_t head_dim, int32_t dtype, const int32_t* kv_indices,
+                const int32_t* kv_flags, const int32_t* kv_counts, int32_t table_width,
+                int32_t global_tokens, int32_t all_queries, float scale_log2, void* workspace,
+                int64_t workspace_bytes, int32_t num_groups, hb_stream_t stream);
 
 /* Paired-table forward that allocates nothing.  No counterpart in the reference: it is for
  * callers that cannot allocate device memory or pass a workspace (code under HIP graph capture,
@@ -199,6 +218,20 @@ int hb_pair_rows(const int32_t* kv_indices, const int32_t* kv_counts, int32_t ro
                  int32_t total_blocks, int32_t key_block_size, int32_t* paired_ids,
                  int32_t* paired_flags, int32_t* paired_counts, int32_t paired_width,
                  int32_t* overflow, hb_stream_t stream);
+
+/* Quad tables for hb_quad_fwd in one launch.  With kv_flags: kv_indices/kv_flags/kv_counts are
+ * paired 64-key tables ([rows, width], rows even; pair_metadata's output, reference
+ * hilberta/paired_metadata.py:26-51) and quad row r is the union of paired rows 2r and 2r + 1,
+ * flag bit 2j + half from paired row 2r + j.  Without (kv_flags NULL): unpaired 64-query tables
+ * (rows a multiple of 4), quad row r the union of rows 4r .. 4r + 3, flag bit j from row 4r + j.
+ * Rows come out ascending and zero padded to quad_width, with counts; a longer union is cut to
+ * quad_width and sets *overflow (device int, may be NULL) to 1.  total_blocks <= 2048.  No
+ * counterpart in the reference: it extends the reference's pairing (paired_metadata.py:38-51)
+ * from two query blocks to four for the 256-query kernel. */
+int hb_quad_rows(const int32_t* kv_indices, const int32_t* kv_flags, const int32_t* kv_counts,
+                 int32_t rows, int32_t width, int32_t total_blocks, int32_t* quad_ids,
+                 int32_t* quad_flags, int32_t* quad_counts, int32_t quad_width, int32_t* overflow,
+                 hb_stream_t stream);
 
 #ifdef __cplusplus
 }
