@@ -16,7 +16,7 @@ def test_library_exports_every_declared_symbol():
     missing = [name for name in declared if not hasattr(lib, name)]
     assert not missing, missing
     assert set(declared) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
-    assert lib.hb_version() == 2
+    assert lib.hb_version() == _lib.header_abi_version() == 3
 
 
 def test_workspace_size_and_rejections():
@@ -30,6 +30,19 @@ def test_workspace_size_and_rejections():
     rc = lib.hb_paired_fwd(None, None, None, None, None, strides, 1, 1, 256, 128, 0, None, None, None,
                            1, 128, 64, 1, 1.0, None, 0, 0, None)
     assert rc == 1 and "null" in _lib.last_error()
+    # quad tables: head_dim 128 and 64-key blocks only; N and G multiples of 256
+    assert lib.hb_attention_workspace_bytes(1, 24, 16896, 128, 512, 28, 64, 2, 1) > 64 * 1024
+    assert lib.hb_attention_workspace_bytes(1, 24, 16896, 64, 512, 28, 64, 2, 1) == -1
+    assert lib.hb_attention_workspace_bytes(1, 24, 16896, 128, 512, 28, 128, 2, 1) == -1
+    assert lib.hb_attention_workspace_bytes(1, 24, 16896 - 128, 128, 512, 28, 64, 2, 1) == -1
+    assert lib.hb_attention_workspace_bytes(1, 24, 16896, 128, 512, 28, 64, 3, 1) == -1
+    rc = lib.hb_quad_rows(None, None, None, 4, 8, 64, None, None, None, 8, None, None)
+    assert rc == 1 and "null" in _lib.last_error()
+    # a lane's output row offset inside an item must fit 32 bits: the output token stride is bounded
+    big = (ctypes.c_int64 * 12)(*([3072] * 11 + [(1 << 31) // 128]))
+    rc = lib.hb_paired_fwd(16, 16, 16, 16, None, big, 1, 1, 256, 128, 0, 16, 16, 16, 1, 128, 64, 1,
+                           1.0, 256, 1 << 20, 0, None)
+    assert rc == 1 and "output token stride" in _lib.last_error()
     rc = lib.hb_hilbert_order(3, None, None)
     assert rc == 1 and "power of two" in _lib.last_error()
     assert lib.hb_plan_scratch_bytes(128, 64) == 256 * 256 * 4
