@@ -82,13 +82,17 @@ def layout_device(grid_size, block_size, text_tokens, shared, device=None):
     nb = n // block_size
     i64 = dict(dtype=torch.int64, device=device)
     t = [torch.empty(n, **i64) for _ in range(4)] + [torch.empty(nb, **i64) for _ in range(2)]
-    status = torch.zeros(2, dtype=torch.int32, device=device)
+    status = torch.zeros(3, dtype=torch.int32, device=device)
     rc = lib.hb_plan_layout(grid_size, block_size, text_tokens, int(bool(shared)),
                             *[x.data_ptr() for x in t], status.data_ptr(), _lib.stream_ptr(device))
     _lib.check(rc, "hb_plan_layout")
-    n_shared, partial = status.tolist()  # setup-time sync: the prefix length is data dependent
+    # setup-time sync: the prefix length is data dependent; the same read checks that the image
+    # order is a permutation, so the per-forward gathers may trust it
+    n_shared, partial, bad_order = status.tolist()
     if partial:
         raise ValueError("Shared square must be a union of complete original blocks")
+    if bad_order:
+        raise RuntimeError("hb_plan_layout produced an image order that is not a permutation")
     return DeviceLayout(grid_size, block_size, text_tokens, n_shared, *t)
 
 
@@ -214,4 +218,32 @@ def pair_rows_device(kv_indices, kv_counts, total_blocks, *, key_block_size=64, 
                                   overflow.data_ptr() if overflow is not None else None,
                                   _lib.stream_ptr(device))
     _lib.check(rc, "hb_pair_rows")
+    return ids, flags, counts
+
+
+def quad_rows_device(kv_indices, kv_counts, total_blocks, *, kv_flags=None, quad_width,
+                     overflow=None):
+    """Quad tables for the 256-query kernel (hb_quad_fwd) in one launch, without a host sync.
+
+    With ``kv_flags``: paired 64-key tables (``pair_metadata``'s output, reference
+    hilberta/paired_metadata.py:26-51); quad row r is the union of paired rows 2r and 2r + 1 with
+    flag bit 2j + half from paired row 2r + j.  Without: unpaired tables, quad row r the union of
+    rows 4r .. 4r + 3 with flag bit j from row 4r + j.  Rows are ascending, zero padded to
+    ``quad_width`` (min(2 * paired width, key blocks) always bounds them); ``overflow`` as in
+    pair_rows_device.  Returns (ids, flags, counts) as int32 device tensors.
+    """
+    _lib.require_gpu(kv_indices, kv_counts)
+    device = kv_indices.device
+    rows, width = kv_indices.shape
+    group = 2 if kv_flags is not None else 4
+    ids = torch.empty((rows // group, quad_width), dtype=torch.int32, device=device)
+    flags = torch.empty_like(ids)
+    counts = torch.empty((rows // group,), dtype=torch.int32, device=device)
+    rc = _lib.load().hb_quad_rows(kv_indices.data_ptr(),
+                                  kv_flags.data_ptr() if kv_flags is not None else None,
+                                  kv_counts.data_ptr(), rows, width, total_blocks, ids.data_ptr(),
+                                  flags.data_ptr(), counts.data_ptr(), quad_width,
+                                  overflow.data_ptr() if overflow is not None else None,
+                                  _lib.stream_ptr(device))
+    _lib.check(rc, "hb_quad_rows")
     return ids, flags, counts

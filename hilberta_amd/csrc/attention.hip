@@ -767,540 +767,6 @@ __global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, 
   }
 }
 
-// Quad tables on a ping-pong schedule: one eight-wave workgroup per CU, 256-query items, each K/V
-// block staged once for all eight waves.  Waves w and w + 4 share a SIMD; group A (waves 0-3) and
-// group B (waves 4-7) run the same steps half a step apart, so that while one group issues its
-// MFMAs (the previous block's O += V^T P^T, then this block's S^T = K Q^T) the other computes its
-// softmax on the VALU, and the two swap at every workgroup barrier:
-//
-//   A:      X M Y V | X M Y V | ...        X = wait for this wave's tile loads, barrier, issue the
-//   B:  X   Y M X V | Y M X V | ...            loads; Y = barrier; M = PV(j - 1), S(j); V = softmax(j)
-//
-// Barrier instances pair up as A.X(j) = B.X(j) (even) and A.Y(j) = B.Y(j) (odd): A's MFMA phase
-// M(j) runs against B's softmax V(j - 1), B's M(j) against A's V(j).  After barrier 2j both
-// groups load K of block j + 1 and V of block j (V is read one step after K, by the PV in
-// M(j + 1)); every wave waits for its loads before barrier 2j + 2.  Those loads overwrite the K of
-// block j - 1 and the V of block j - 2, whose last readers (S(j - 1) in M(j - 1), PV(j - 2) in
-// M(j - 1)) both groups finished before barrier 2j, so two K and two V stages (64 KiB) suffice.
-// The per-query arithmetic is that of attn_fwd_kernel (same blocks, order, masking and rounding):
-// ordinary rows are bitwise equal.
-template <bool F16>
-__global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnArgs a) {
-  constexpr int D = 128, WAVES = 8, QT = 256, QW = 32;
-  constexpr int CPR = D / 8, TILE = KEYS * D, DT = D / 32, DS = D / 16;
-  constexpr int FRAG = DT * 16 * 64, VW = WAVES;
-  // Where each wave issues the two halves of its tile loads: 0 = right after its barrier, 1 =
-  // between its PV and score MFMAs (group A only), 2 = at the start of its softmax, 3 = before its
-  // exponentials.
-  constexpr int POS_A0 = 0, POS_A1 = 0, POS_B0 = 0, POS_B1 = 0;
-  constexpr int LOADERS = 8;
-  // two K stages, then two V stages (all LDS offsets fit the 16-bit DS immediate)
-  __shared__ __attribute__((aligned(1024))) uint16_t ldk0[TILE];
-  __shared__ __attribute__((aligned(1024))) uint16_t ldk1[TILE];
-  __shared__ __attribute__((aligned(1024))) uint16_t ldv0[TILE];
-  __shared__ __attribute__((aligned(1024))) uint16_t ldv1[TILE];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool grp_b = wave >= 4;
-  const int half = wave >> 1;  // 64-query block of the item: the flag bit this wave tests
-  const int ql = lane & 31;
-  const int hl = lane >> 5;
-
-  // ------------------------------------------------------------------ persistent work queues
-  // As in attn_fwd_kernel: 8 queues (one per XCD), global chunks first, the first two items of
-  // every workgroup dealt out, later ones claimed one item ahead with the queue's atomic counter.
-  __shared__ int s_claim[2];
-  constexpr int nq = QUEUES;
-  const int qx = blockIdx.x % nq;
-  const int gper = a.global_tiles * a.nsplit;
-  const int total_g = a.bh * gper;
-  const int total_r = a.bh * a.rows;
-  auto g_lo = [&](int q) __attribute__((always_inline)) { return (int)((int64_t)total_g * q / nq); };
-  auto r_lo = [&](int q) __attribute__((always_inline)) { return (int)((int64_t)total_r * q / nq); };
-  auto item_of = [&](int q, int c) __attribute__((always_inline)) {
-    const int gl = g_lo(q + 1) - g_lo(q);
-    if (c < gl) return g_lo(q) + c;
-    c -= gl;
-    return c < r_lo(q + 1) - r_lo(q) ? total_g + r_lo(q) + c : -1;
-  };
-  auto dealt = [&](int q) __attribute__((always_inline)) { return ((int)gridDim.x - q + nq - 1) / nq; };
-  const bool all_dealt =
-      2 * ((int)gridDim.x / nq) >= (total_g + nq - 1) / nq + (total_r + nq - 1) / nq;
-  auto claim_from = [&](int first_count) __attribute__((always_inline)) {
-    if (all_dealt) return -1;
-    const int own = item_of(qx, 2 * dealt(qx) + first_count);
-    if (own >= 0) return own;
-    unsigned* mask = (unsigned*)&a.counters[QUEUES + 1];
-    const unsigned drained = atomicOr(mask, 1u << qx);
-    for (int t = 1; t < nq; ++t) {
-      const int q = (qx + t) % nq;
-      if ((drained >> q) & 1) continue;
-      const int c = item_of(q, 2 * dealt(q) + atomicAdd(&a.counters[q], 1));
-      if (c >= 0) return c;
-    }
-    return -1;
-  };
-  if (tid == 0) {
-    const int rank = ((int)blockIdx.x / nq + dealt(qx) / 2) % dealt(qx);
-    int i0 = item_of(qx, rank), i1 = item_of(qx, rank + dealt(qx));
-    if (i0 < 0 && !all_dealt) i0 = claim_from(atomicAdd(&a.counters[qx], 1));
-    if (i1 < 0 && !all_dealt) i1 = claim_from(atomicAdd(&a.counters[qx], 1));
-    s_claim[0] = i0;
-    s_claim[1] = i1;
-  }
-  __syncthreads();
-
-  struct Item {
-    int valid, bh, b, h, global, qfirst, row, gtile, split, first_block, nsteps;
-  };
-  auto decode = [&](int idx) __attribute__((always_inline)) {
-    Item it;
-    it.valid = idx >= 0;
-    const int i = it.valid ? idx : 0;
-    it.global = i < total_g;
-    it.row = 0;
-    it.gtile = 0;
-    it.split = 0;
-    it.first_block = 0;
-    if (it.global) {
-      it.bh = i / gper;
-      const int rem = i - it.bh * gper;
-      it.gtile = rem / a.nsplit;
-      it.split = rem - it.gtile * a.nsplit;
-      it.qfirst = it.gtile * QT;
-      it.first_block = it.split * a.chunk;
-      it.nsteps = min(a.chunk, a.key_blocks - it.first_block);
-    } else {
-      const int ri = i - total_g;
-      it.bh = ri / a.rows;
-      it.row = ri - it.bh * a.rows;
-      it.qfirst = a.tokens - (a.rows - it.row) * QT;
-      it.nsteps = 0;
-    }
-    it.b = it.bh / a.heads;
-    it.h = it.bh - it.b * a.heads;
-    return it;
-  };
-  auto load_meta = [&](const Item& it, int& cnt, int& t_id, int& t_fl) __attribute__((always_inline)) {
-    cnt = 0;
-    t_id = 0;
-    t_fl = 0;
-    if (!it.valid || it.global) return;
-    const int64_t row = (int64_t)it.row * a.width;
-    cnt = a.counts[it.row];
-    t_id = row_entry(a.indices + row, a.width, lane);
-    t_fl = row_entry(a.flags + row, a.width, lane);
-  };
-
-  Item cur = decode(uniform(s_claim[0]));
-  int nxt_idx = uniform(s_claim[1]);
-  int c_cnt, t_id, t_fl, n_cnt, n_id, n_fl;
-  load_meta(cur, c_cnt, t_id, t_fl);
-  load_meta(decode(nxt_idx), n_cnt, n_id, n_fl);
-  if (!cur.global) cur.nsteps = max(uniform(c_cnt), 1);
-  int tbase = 0;
-  int pending = 0;
-  bool claiming = false;
-
-  auto step_info = [&](int s, int& kb, int& fl) __attribute__((always_inline)) {
-    if (cur.global) {
-      kb = cur.first_block + s;
-      fl = 15;
-      return;
-    }
-    if (s >= tbase + 64) {
-      tbase = s & ~63;
-      const int64_t row = (int64_t)cur.row * a.width;
-      t_id = row_entry(a.indices + row, a.width, tbase + lane);
-      t_fl = row_entry(a.flags + row, a.width, tbase + lane);
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    }
-    kb = __builtin_amdgcn_readlane(t_id, s - tbase);
-    fl = __builtin_amdgcn_readlane(t_fl, s - tbase) & 15;
-  };
-
-  u32x4 qreg[DS];
-  auto load_q = [&](const Item& it) __attribute__((always_inline)) {
-    const uint16_t* qp = a.q + (int64_t)it.b * a.q_sb + (int64_t)it.h * a.q_sh +
-                         (int64_t)(it.qfirst + wave * QW + ql) * a.q_sn + hl * 8;
-#pragma unroll
-    for (int ds = 0; ds < DS; ++ds) qreg[ds] = *(const u32x4*)(qp + ds * 16);
-  };
-
-  // Tile loads: each of the eight waves issues two K and two V instructions (1 KiB each) per block.
-  constexpr int NDMA = CPR / LOADERS;
-  constexpr int ROWS_PER_ROUND = LOADERS * 64 / CPR;
-  static_assert(CPR % LOADERS == 0 && ROWS_PER_ROUND % 16 == 0, "linear tile-load offsets");
-  int dk, dv;
-  {
-    const int slot = (wave % LOADERS) * 64 + lane;
-    const int r = slot / CPR;
-    const int c = (slot % CPR) ^ swz<CPR>(r);
-    dk = (int)(r * a.k_sn + c * 8) * 2;
-    dv = (int)(r * a.v_sn + c * 8) * 2;
-  }
-  auto k_base = [&](const Item& it) __attribute__((always_inline)) { return a.k + (int64_t)it.b * a.k_sb + (int64_t)it.h * a.k_sh; };
-  auto v_base = [&](const Item& it) __attribute__((always_inline)) { return a.v + (int64_t)it.b * a.v_sb + (int64_t)it.h * a.v_sh; };
-  const int kblk_bytes = KEYS * (int)a.k_sn * 2, vblk_bytes = KEYS * (int)a.v_sn * 2;
-  const int kround_bytes = ROWS_PER_ROUND * (int)a.k_sn * 2;
-  const int vround_bytes = ROWS_PER_ROUND * (int)a.v_sn * 2;
-  auto dma_k = [&](uint16_t* dst, const uint16_t* kbase, int kb) __attribute__((always_inline)) {
-    const int sk = kb * kblk_bytes;
-    int w = wave % LOADERS;
-    asm volatile("" : "+s"(w));
-#pragma unroll
-    for (int n = 0; n < NDMA; ++n)
-      buffer_load_lds16(kbase, dst + (n * LOADERS + w) * 512, dk, sk + n * kround_bytes);
-  };
-  auto dma_v = [&](uint16_t* dst, const uint16_t* vbase, int kb) __attribute__((always_inline)) {
-    const int sv = kb * vblk_bytes;
-    int w = wave % LOADERS;
-    asm volatile("" : "+s"(w));
-#pragma unroll
-    for (int n = 0; n < NDMA; ++n)
-      buffer_load_lds16(vbase, dst + (n * LOADERS + w) * 512, dv, sv + n * vround_bytes);
-  };
-
-  int koff[DS];
-#pragma unroll
-  for (int ds = 0; ds < DS; ++ds) koff[ds] = ql * D + (((2 * ds + hl) ^ swz<CPR>(ql)) << 3);
-  int voff[DT][2];
-  {
-    const int g = lane >> 4, j = (lane >> 2) & 3, t = lane & 3;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        const int row = 4 * hl + j + 8 * rb;
-        const int d = 32 * dt + 16 * (g & 1) + 4 * t;
-        voff[dt][rb] = row * D + (((d >> 3) ^ swz<CPR>(row)) << 3) + (d & 7);
-      }
-  }
-
-  f32x16 acc[DT];
-  float m_run = -__builtin_inff(), l_run = 0.f;
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
-  f32x16 sc[2];   // scores of the block the last M phase computed
-  u32x4 pk[4];    // its P, packed, for the next M phase's PV MFMAs
-
-  // Epilogue target of the item whose last PV is pending (set when the cursor leaves it).
-  uint16_t* e_o = nullptr;
-  float* e_l = nullptr;
-  int64_t e_slot = 0;
-  bool e_part = false;
-  auto set_epilogue = [&](const Item& it) __attribute__((always_inline)) {
-    e_part = it.global && a.nsplit > 1;
-    const int tile = it.bh * a.global_tiles + it.gtile;
-    e_slot = ((int64_t)tile * a.nsplit + it.split) * VW + wave;
-    e_o = a.o + (int64_t)it.b * a.o_sb + (int64_t)it.h * a.o_sh + (int64_t)it.qfirst * a.o_sn;
-    e_l = a.lse ? a.lse + (int64_t)it.bh * a.tokens + it.qfirst : nullptr;
-  };
-  const int o_lane = (wave * QW + ql) * a.o_sn + hl * 8;
-  const int l_lane = wave * QW + ql;
-  auto epilogue = [&]() __attribute__((always_inline)) {
-    const float l_tot = pair_sum(l_run);
-    if (!e_part) {
-      const float inv = 1.f / l_tot;
-      uint16_t* op = e_o + o_lane;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int gp = 0; gp < 2; ++gp) {
-          const u32x2 ea = u32x2{pack2<F16>(acc[dt][8 * gp + 0] * inv, acc[dt][8 * gp + 1] * inv),
-                                 pack2<F16>(acc[dt][8 * gp + 2] * inv, acc[dt][8 * gp + 3] * inv)};
-          const u32x2 ob = u32x2{pack2<F16>(acc[dt][8 * gp + 4] * inv, acc[dt][8 * gp + 5] * inv),
-                                 pack2<F16>(acc[dt][8 * gp + 6] * inv, acc[dt][8 * gp + 7] * inv)};
-          const auto x = __builtin_amdgcn_permlane32_swap(ea[0], ob[0], false, false);
-          const auto y = __builtin_amdgcn_permlane32_swap(ea[1], ob[1], false, false);
-          const unsigned x0 = x[0], x1 = x[1], y0 = y[0], y1 = y[1];
-          *(u32x4*)(op + dt * 32 + gp * 16) = u32x4{x0, y0, x1, y1};
-        }
-      if (e_l && hl == 0) e_l[l_lane] = (m_run + __log2f(l_tot)) * LN2;
-      return;
-    }
-    float* pa = a.part + e_slot * FRAG;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) pa[(dt * 16 + i) * 64 + lane] = acc[dt][i];
-    float* pml = a.part_ml + e_slot * 128;
-    pml[lane] = m_run;
-    pml[64 + lane] = l_tot;
-  };
-
-  // ------------------------------------------------------------------ phases
-  const uint16_t* cur_k = k_base(cur);
-  const uint16_t* cur_v = v_base(cur);
-  int s = 0;             // cursor: the step of `cur` whose scores the next M phase computes
-  int c_kb = 0, c_fl = 0;  // its block and flags
-  int v_fl = 0;          // flags of the block whose scores sc holds (the next softmax)
-  int la_kb = 0, la_fl = 0;  // block and flags of the step after the cursor (K loaded by the last X)
-  bool la_cross = false; // that step starts the next item
-  bool epi_pending = false;  // the next PV completes the item set_epilogue recorded
-  bool meta_new = false;     // nxt_idx was just claimed and its table entries are not loaded yet
-  bool vm_late = false;      // eight or more vector memory operations followed the last tile loads
-
-  // Xw: wait for this wave's tile loads, barrier, take a pending claim.  The wait leaves the last
-  // eight operations in flight when they are output stores or the next item's Q (issued after the
-  // tile loads, so the tile loads are complete either way).
-  auto Xw = [&]() __attribute__((always_inline)) {
-    if (claiming && tid == 0) s_claim[0] = claim_from(pending);
-    if (vm_late) __builtin_amdgcn_s_waitcnt(0x0078);  // vmcnt(8) lgkmcnt(0)
-    else __builtin_amdgcn_s_waitcnt(0x0070);          // vmcnt(0) lgkmcnt(0)
-    vm_late = false;
-    asm volatile("s_barrier" ::: "memory");
-    if (claiming) {
-      claiming = false;
-      nxt_idx = uniform(s_claim[0]);
-      meta_new = true;
-    }
-  };
-  // XL: issue this wave's share of the loads of the K tile of the step after the cursor into
-  // `kdst` and of the V tile of the cursor step into `vdst`.
-  // XLc: block and flags of the step after the cursor, and the sources of this step's tile loads:
-  // K of the step after the cursor, V of the cursor step.  issue(n) then issues the n-th K and V
-  // instructions of this wave (n = 0, 1).
-  const uint16_t* ld_kb = cur_k;
-  const uint16_t* ld_vb = cur_v;
-  int ld_ko = 0, ld_vo = 0;
-  auto XLc = [&]() __attribute__((always_inline)) {
-    ld_vb = cur_v;
-    ld_vo = c_kb * vblk_bytes;
-    la_cross = s + 1 >= cur.nsteps;
-    ld_kb = cur_k;
-    ld_ko = 0;
-    if (!la_cross) {
-      step_info(s + 1, la_kb, la_fl);
-      ld_ko = la_kb * kblk_bytes;
-    } else if (nxt_idx >= 0) {
-      if (meta_new) {
-        load_meta(decode(nxt_idx), n_cnt, n_id, n_fl);
-        meta_new = false;
-      }
-      const Item nx = decode(nxt_idx);
-      la_kb = nx.global ? nx.first_block : __builtin_amdgcn_readlane(n_id, 0);
-      la_fl = nx.global ? 15 : __builtin_amdgcn_readlane(n_fl, 0) & 15;
-      ld_kb = k_base(nx);
-      ld_ko = la_kb * kblk_bytes;
-    }
-    if (meta_new) {
-      load_meta(decode(nxt_idx), n_cnt, n_id, n_fl);
-      meta_new = false;
-    }
-  };
-  auto issue = [&](int n, uint16_t* kdst, uint16_t* vdst) __attribute__((always_inline)) {
-    int w = wave % LOADERS;
-    asm volatile("" : "+s"(w));
-    buffer_load_lds16(ld_kb, kdst + (n * LOADERS + w) * 512, dk, ld_ko + n * kround_bytes);
-    buffer_load_lds16(ld_vb, vdst + (n * LOADERS + w) * 512, dv, ld_vo + n * vround_bytes);
-  };
-  auto Y = [&]() __attribute__((always_inline)) { asm volatile("s_barrier" ::: "memory"); };
-
-  // The cursor moves to the step the last X loaded; at the end of an item it records the item's
-  // epilogue, switches to the next one (its Q is loaded here: the current Q is dead after the
-  // score MFMAs) and claims the item after it.  Returns false when no step is left.
-  auto advance = [&]() __attribute__((always_inline)) -> bool {
-    if (!la_cross) {
-      ++s;
-      c_kb = la_kb;
-      c_fl = la_fl;
-      return true;
-    }
-    set_epilogue(cur);
-    epi_pending = true;
-    if (nxt_idx < 0) return false;
-    cur = decode(nxt_idx);
-    cur_k = k_base(cur);
-    cur_v = v_base(cur);
-    t_id = n_id;
-    t_fl = n_fl;
-    tbase = 0;
-    if (!cur.global) cur.nsteps = max(uniform(n_cnt), 1);
-    s = 0;
-    c_kb = la_kb;
-    c_fl = la_fl;
-    load_q(cur);
-    vm_late = true;
-    if (tid == 0 && !all_dealt) pending = atomicAdd(&a.counters[qx], 1);
-    claiming = true;
-    return true;
-  };
-
-  // PV of the previous block (V tile at `vt`, P in pk).  Before the first block pk is zero and
-  // the V stage holds zeros, so the first PV adds exact zeros.
-  auto pv_mfmas = [&](const uint16_t* vt) __attribute__((always_inline)) {
-    constexpr int NPV = 4 * DT;
-    u32x4 vr[NPV];
-    auto vread = [&](int j) __attribute__((always_inline)) {
-      const int dt = j % DT, ks = j / DT;
-      const u32x2 lo = read_tr(vt + voff[dt][0] + ks * 16 * D);
-      const u32x2 hi = read_tr(vt + voff[dt][1] + ks * 16 * D);
-      return u32x4{lo[0], lo[1], hi[0], hi[1]};
-    };
-#pragma unroll
-    for (int j = 0; j < PFV; ++j) vr[j] = vread(j);
-#pragma unroll
-    for (int j = 0; j < NPV; ++j) {
-      if (j + PFV < NPV) vr[j + PFV] = vread(j + PFV);
-      acc[j % DT] = mfma32<F16>(vr[j], pk[j / DT], acc[j % DT]);
-    }
-#pragma unroll
-    for (int j = 0; j < NPV - PFV; ++j) {
-      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(SG_MFMA, PFV, 0);
-  };
-  // M: PV of the previous block (V in `vt`), then the scores of the cursor block (K in `kt`).
-  auto M = [&](const uint16_t* vt, const uint16_t* kt, auto&& mid) __attribute__((always_inline)) {
-    pv_mfmas(vt);
-    mid();
-    sc[0] = sc[1] = f32x16{};
-    u32x4 kr[2 * DS];
-#pragma unroll
-    for (int ds = 0; ds < 2; ++ds) {
-      kr[2 * ds] = *(const u32x4*)(kt + koff[ds]);
-      kr[2 * ds + 1] = *(const u32x4*)(kt + koff[ds] + 32 * D);
-    }
-#pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-      if (ds + 2 < DS) {
-        kr[2 * ds + 4] = *(const u32x4*)(kt + koff[ds + 2]);
-        kr[2 * ds + 5] = *(const u32x4*)(kt + koff[ds + 2] + 32 * D);
-      }
-      sc[0] = mfma32<F16>(kr[2 * ds], qreg[ds], sc[0]);
-      sc[1] = mfma32<F16>(kr[2 * ds + 1], qreg[ds], sc[1]);
-    }
-    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 4, 0);
-#pragma unroll
-    for (int ds = 0; ds < DS - 2; ++ds) {
-      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4, 0);
-    if (epi_pending) {
-      epilogue();
-      vm_late = true;
-      epi_pending = false;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
-      m_run = -__builtin_inff();
-      l_run = 0.f;
-    }
-    v_fl = c_fl;
-  };
-
-  // Online softmax of the scores in sc (this lane: 32 of query ql's 64 keys), as in
-  // attn_fwd_kernel; P goes to pk for the next M phase.
-  auto V = [&](auto&& start, auto&& before_exp) __attribute__((always_inline)) {
-    start();
-    const bool live = (v_fl >> half) & 1;
-    float m = sc[0][0];
-#pragma unroll
-    for (int i = 1; i < 16; ++i) m = fmaxf(m, sc[0][i]);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) m = fmaxf(m, sc[1][i]);
-    const float mx = live ? m * a.scale_log2 : -__builtin_inff();
-    if (__ballot(mx > m_run + RESCALE_LOG2) != 0) {
-      const float m_new = fmaxf(m_run, pair_max(mx));
-      const float alpha = fast_exp2(m_run - m_new);
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
-      m_run = m_new;
-    }
-    before_exp();
-    const float neg = live ? -m_run : -__builtin_inff();
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sc[t][i] = fast_exp2(__builtin_fmaf(sc[t][i], a.scale_log2, neg));
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      pk[2 * t] = pack8<F16>(f32x8{sc[t][0], sc[t][1], sc[t][2], sc[t][3], sc[t][4], sc[t][5],
-                                   sc[t][6], sc[t][7]});
-      pk[2 * t + 1] = pack8<F16>(f32x8{sc[t][8], sc[t][9], sc[t][10], sc[t][11], sc[t][12],
-                                       sc[t][13], sc[t][14], sc[t][15]});
-    }
-    float ls[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) ls[i & 3] += sc[t][i];
-    l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
-  };
-
-  // Step j of parity p = j % 2: S reads K stage p, the PV reads V stage 1 - p (block j - 1).  The
-  // loads that follow A's barrier (before its M) take K of block j + 1 into stage 1 - p and V of
-  // block j into stage p; those that follow B's barrier (after its M, the cursor already on step
-  // j + 1) K of block j + 2 into stage p and V of block j + 1 into stage 1 - p.
-  auto iter = [&](uint16_t* __restrict__ kp, uint16_t* __restrict__ kq, uint16_t* __restrict__ vp,
-                  uint16_t* __restrict__ vq) __attribute__((always_inline)) -> bool {
-    // this wave's load destinations: A loads into kq / vp, B (one step ahead) into kp / vq
-    auto at = [&](int pos) __attribute__((always_inline)) {
-      if (!grp_b) {
-        if (POS_A0 == pos) issue(0, kq, vp);
-        if (POS_A1 == pos) issue(1, kq, vp);
-      } else {
-        if (POS_B0 == pos) issue(0, kp, vq);
-        if (POS_B1 == pos) issue(1, kp, vq);
-      }
-    };
-    bool b_loads = false;  // group B issued its barrier and computed loads this step
-    if (!grp_b) {
-      Xw();
-      XLc();
-      at(0);
-    }
-    M(vq, kp, [&]() __attribute__((always_inline)) { if (!grp_b) at(1); });
-    const bool more = advance();
-    if (grp_b && more) {
-      Xw();
-      XLc();
-      at(0);
-      b_loads = true;
-    }
-    V([&]() __attribute__((always_inline)) { if (!grp_b || b_loads) at(2); },
-      [&]() __attribute__((always_inline)) { if (!grp_b || b_loads) at(3); });
-    if (more) return false;
-    // the last block's V tile (loaded by the last XL) in every wave's view, its PV, the epilogue
-    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
-    asm volatile("s_barrier" ::: "memory");
-    pv_mfmas(vp);
-    epilogue();
-    return true;
-  };
-
-  if (cur.valid) {
-    // zero P and V stage 1, which the first PV reads, so that PV adds exact zeros
-#pragma unroll
-    for (int t = 0; t < 4; ++t) pk[t] = u32x4{0u, 0u, 0u, 0u};
-    for (int i = tid; i < TILE / 8; i += 512) *(u32x4*)(ldv1 + 8 * i) = u32x4{0u, 0u, 0u, 0u};
-    load_q(cur);
-    step_info(0, c_kb, c_fl);
-    dma_k(ldk0, cur_k, c_kb);
-    if (grp_b) {
-      // B's first loads: K of block 1, V of block 0, all of them now
-      Xw();
-      XLc();
-      issue(0, ldk1, ldv0);
-      issue(1, ldk1, ldv0);
-    }
-    for (;;) {
-      if (iter(ldk0, ldk1, ldv0, ldv1)) break;
-      if (iter(ldk1, ldk0, ldv1, ldv0)) break;
-    }
-  }
-  // the last workgroup to leave resets the queue counters for the next launch
-  __syncthreads();
-  if (tid == 0 && atomicAdd(&a.counters[QUEUES], 1) == (int)gridDim.x - 1) {
-    for (int q = 0; q <= QUEUES + 1; ++q) atomicExch(&a.counters[q], 0);
-  }
-}
-
 // Combines the chunks of each split global query tile: O = sum_c 2^(m_c - M) acc_c / L with
 // M = max_c m_c and L = sum_c 2^(m_c - M) l_c; LSE = (M + log2 L) ln 2.  One workgroup per tile,
 // thread (wave, lane) owning the same fragment registers as in attn_fwd_kernel.
@@ -1456,11 +922,8 @@ __global__ __launch_bounds__(64) void clear_counters_kernel(int32_t* counters) {
 
 template <int HALVES, int D, int KBR, bool F16>
 void launch(const AttnArgs& a, int groups, hipStream_t stream) {
-  if constexpr (HALVES == 4)
-    hipLaunchKernelGGL((attn_pp_kernel<F16>), dim3(groups), dim3(512), 0, stream, a);
-  else
-    hipLaunchKernelGGL((attn_fwd_kernel<HALVES, D, KBR, F16>), dim3(groups), dim3(128 * HALVES), 0,
-                       stream, a);
+  hipLaunchKernelGGL((attn_fwd_kernel<HALVES, D, KBR, F16>), dim3(groups), dim3(128 * HALVES), 0,
+                     stream, a);
   const int tiles = a.bh * a.global_tiles;
   if (a.nsplit > 1 && tiles > 0)
     hipLaunchKernelGGL((merge_kernel<HALVES, D, F16>), dim3(tiles, D / 32), dim3(128 * HALVES), 0,

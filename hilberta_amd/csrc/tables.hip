@@ -66,7 +66,8 @@ __global__ void composite_kernel(int g, int64_t* original, int64_t* inverse) {
 }
 
 // One workgroup: classify original blocks as shared (inside the centre square) or ordinary, then
-// pack them stably: shared blocks first (plan.py:138-150).  status[0] = #shared, [1] = partial.
+// pack them stably: shared blocks first (plan.py:138-150).  status[0] = #shared, [1] = partial,
+// [2] cleared for order_check_kernel.
 __global__ void __launch_bounds__(1024) pack_blocks_kernel(int g, int bs, int shared,
                                                            const int64_t* original, int text_blocks,
                                                            int64_t* packed, int64_t* to_physical,
@@ -124,6 +125,7 @@ __global__ void __launch_bounds__(1024) pack_blocks_kernel(int g, int bs, int sh
   if (t == 0) {
     status[0] = n_shared;
     status[1] = s_total[1];
+    status[2] = 0;  // set by order_check_kernel if the image order is no permutation
   }
 }
 
@@ -133,7 +135,17 @@ __global__ void image_order_kernel(int64_t n, int bs, const int64_t* original, c
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t tok = original[packed[i / bs] * bs + i % bs];
     order[i] = tok;
-    inverse_order[tok] = i;
+    if (tok >= 0 && tok < n) inverse_order[tok] = i;
+  }
+}
+
+// status[2] = 1 unless order is a permutation of [0, n) (then inverse_order[order[i]] = i for
+// every i; two positions holding one token leave one of them unmatched).
+__global__ void order_check_kernel(int64_t n, const int64_t* order, const int64_t* inverse_order,
+                                   int32_t* status) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t tok = order[i];
+    if (tok < 0 || tok >= n || inverse_order[tok] != i) atomicOr(&status[2], 1);
   }
 }
 
@@ -382,6 +394,8 @@ extern "C" int hb_plan_layout(int32_t grid_size, int32_t block_size, int32_t tex
   hipLaunchKernelGGL(image_order_kernel, dim3(grid_for(n)), dim3(TPB), 0, stream, n, block_size,
                      (const int64_t*)original_order, (const int64_t*)physical_original_blocks,
                      image_order, inverse_image_order);
+  hipLaunchKernelGGL(order_check_kernel, dim3(grid_for(n)), dim3(TPB), 0, stream, n,
+                     (const int64_t*)image_order, (const int64_t*)inverse_image_order, status);
   HB_HIP(hipGetLastError());
   return HB_OK;
 }

@@ -30,17 +30,28 @@ def _outer_stride(x, dim):
     return outer, dims[-1][1]
 
 
-def index_select_rows(x, dim, index, *, out=None, error=None):
+def index_select_rows(x, dim, index, *, out=None, error=None, check=False):
     """Gather rows of ``x`` along ``dim`` by ``index`` (int64, on x's device) with the HIP kernel.
 
-    ``error`` may be a device int32 scalar tensor that is set to 1 if an index was out of range
-    (such rows are left unwritten); without it, indices are trusted (validated at plan setup).
-    Without ``out`` and ``error`` this is the operator ``torch.ops.hilberta_hip.gather_rows``.
+    Indices are trusted by default: the persistent-layout orders come from the plan builder,
+    which checks them once (every order it returns is a permutation of the image tokens), and the
+    per-forward gather must not synchronise.  An out-of-range index is then skipped (its row of
+    the output is left unwritten; nothing outside ``x`` or the output is touched).  ``check=True``
+    raises IndexError as ``index_select`` does (reference flux_adapter.py:209-212), at the cost of
+    one host synchronisation.  ``error`` may instead be a device int32 scalar tensor that the
+    kernel sets to 1 on an out-of-range index, for callers that check it later.  Without ``out``,
+    ``error`` and ``check`` this is the operator ``torch.ops.hilberta_hip.gather_rows``.
     """
     _lib.require_gpu(x, index)
     dim = dim % x.ndim
     if index.dtype != torch.int64 or index.ndim != 1 or index.device != x.device:
         raise ValueError("index must be a 1-D int64 tensor on x's device")
+    if check:
+        err = torch.zeros(1, dtype=torch.int32, device=x.device) if error is None else error
+        res = gather_into(x, dim, index, out=out, error=err)
+        if int(err.item()):
+            raise IndexError("index out of range in self")
+        return res
     if out is None and error is None:
         from . import ops
 

@@ -22,7 +22,8 @@ from .sparse_kernel import (
 )
 
 
-# Persistent workgroup count for hb_paired_fwd; 0 lets the library choose (2 per compute unit).
+# Persistent workgroup count for hb_paired_fwd; 0 lets the library choose (2 per compute unit; 3
+# for D = 64 calls with at least two items per workgroup).
 NUM_GROUPS = 0
 
 

@@ -2,8 +2,9 @@
 
 Drop-in for reference hilberta/paired_metadata.py.  ``PairedMetadata`` is the same frozen
 carrier (paired_metadata.py:8-23).  ``pair_metadata`` keeps its signature and CPU validation
-(validate_metadata) but does the merge itself on the GPU with the HIP kernel hb_pair_tables:
-for paired row r the key blocks of query blocks 2r and 2r+1 are unioned in ascending block
+(validate_metadata) but does the merge itself on the GPU with the HIP table kernels (the rows
+become adjacency bitmaps, hb_table_bits; paired rows are counted and emitted from them,
+hb_bits_counts / hb_bits_emit): for paired row r the key blocks of query blocks 2r and 2r+1 are unioned in ascending block
 order and each key block gets flag bit (half + 2*key_half) for every (query half, 64-key half)
 that sees it (paired_metadata.py:26-51).  Tables come back on the CPU, as in the reference, so
 callers keep their own ``.to(device)`` caching; ``pair_metadata_device`` keeps them on the GPU.

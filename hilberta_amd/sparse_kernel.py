@@ -23,7 +23,8 @@ import torch
 LOG2E = 1.4426950408889634
 
 # Persistent workgroup count for the attention launches of sparse_attention; 0 lets the library
-# choose (2 per compute unit).
+# choose (2 per compute unit; 3 for paired D = 64 calls with at least two items per workgroup,
+# which covers pairable tables, since sparse_attention runs those on the paired kernel).
 NUM_GROUPS = 0
 
 

@@ -171,7 +171,8 @@ int hb_hilbert_order(int32_t grid_size, int64_t* out, hb_stream_t stream);
 /* Composite order and physical packing (reference hilberta/plan.py:133-150, :186-197):
  * original_order / inverse_original [n], image_order / inverse_image_order [n],
  * physical_original_blocks [nb] (shared blocks first) and original_to_physical [nb] (+ text
- * blocks).  status (device int32[2]) receives {#shared blocks, partial-shared-block flag}. */
+ * blocks).  status (device int32[3]) receives {#shared blocks, partial-shared-block flag,
+ * 1 if image_order is not a permutation of the image tokens (else 0)}. */
 int hb_plan_layout(int32_t grid_size, int32_t block_size, int32_t text_tokens, int32_t shared,
                    int64_t* original_order, int64_t* inverse_original, int64_t* image_order,
                    int64_t* inverse_image_order, int64_t* physical_original_blocks,

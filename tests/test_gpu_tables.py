@@ -166,6 +166,41 @@ def test_index_select_rows_strided_and_errors(hip_device):
         index_select_rows(x.transpose(2, 3), 1, index)  # row not contiguous
 
 
+def test_index_select_rows_out_of_range_contract(hip_device):
+    """check=True raises as index_select does (flux_adapter.py:209-212); the default trusts the
+    index (plan orders are checked once at build), skips an out-of-range row, and writes every
+    in-range row exactly as index_select would."""
+    from hilberta_amd.layout import index_select_rows
+
+    x = torch.randn(2, 512, 64, device=hip_device).to(torch.bfloat16)
+    index = torch.randperm(512, device=hip_device)
+    assert torch.equal(index_select_rows(x, 1, index, check=True), x.index_select(1, index))
+    for bad_value in (512, -1, 1 << 40):
+        bad = index.clone()
+        bad[7] = bad_value
+        with pytest.raises(IndexError, match="out of range"):
+            index_select_rows(x, 1, bad, check=True)
+        out = torch.full((2, 512, 64), 3.0, device=hip_device).to(torch.bfloat16)
+        index_select_rows(x, 1, bad, out=out)
+        keep = torch.ones(512, dtype=torch.bool, device=hip_device)
+        keep[7] = False
+        assert torch.equal(out[:, keep], x.index_select(1, index[keep]))
+        assert torch.equal(out[:, 7], torch.full_like(out[:, 7], 3.0))  # left unwritten
+
+
+@pytest.mark.parametrize("grid,tiles,shared", [(64, 4, False), (128, 16, False), (64, 16, True)])
+def test_plan_orders_are_checked_permutations(hip_device, grid, tiles, shared):
+    """The layout builder's orders (validated on the device at build time) are inverse
+    permutations, so the per-forward gathers may trust them."""
+    from hilberta_amd._tables import layout_device
+
+    lay = layout_device(grid, 64, 512, shared, device=hip_device)
+    n = grid * grid
+    ar = torch.arange(n, device=hip_device)
+    assert torch.equal(torch.sort(lay.image_order).values, ar)
+    assert torch.equal(lay.inverse_image_order[lay.image_order], ar)
+
+
 def test_plan_layout_permutes_latents(hip_device):
     """Permute at entry, unpermute at exit with the device plan's orders (sampling_layout.py:88-116)."""
     from hilberta_amd.bridge_k import paired_plan_device
