@@ -417,6 +417,153 @@ def denoiser_bench(a):
     print(json.dumps(result), flush=True)
 
 
+def mfma_peak_tflops(stream, reps=5):
+    """Dense bf16 MFMA rate this GPU sustains now: hb_mfma_peak_probe (back-to-back
+    v_mfma_f32_32x32x16_bf16 on every SIMD, about a millisecond per launch), median of `reps`
+    event-timed launches after one warmup."""
+    import ctypes
+
+    from hilberta_amd import _lib
+
+    lib = _lib.load()
+    groups = 2 * torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.empty(groups * 256, dtype=torch.float32, device="cuda:0")
+    flops = ctypes.c_int64(0)
+    iters = 8192
+
+    def run():
+        _lib.check(lib.hb_mfma_peak_probe(iters, groups, sink.data_ptr(), ctypes.byref(flops),
+                                          stream.cuda_stream), "hb_mfma_peak_probe")
+
+    run()
+    ms = statistics.median(event_time(run, reps, stream))
+    return flops.value / (ms * 1e-3) / 1e12, ms
+
+
+def sampled_parity(out, lse, q, k, v, rows, G, scale, picks):
+    """parity_check restricted to a sample: the first and last 64 global rows and the ordinary
+    64-query rows `picks` (indices into `rows`), each against fp32 attention recomputed on the
+    device from the tables."""
+    kf, vf = k.float(), v.float()
+    errs = []
+    segs = [(0, 64, None), (G - 64, G, None)] if G >= 128 else ([(0, G, None)] if G else [])
+    segs += [(G + 64 * r, G + 64 * r + 64, rows[r]) for r in picks]
+    offs = torch.arange(64, device=out.device)
+    for q0, q1, blocks in segs:
+        if blocks is None:
+            kk, vv = kf, vf
+        else:
+            cols = (torch.tensor(blocks, device=out.device)[:, None] * 64 + offs).reshape(-1)
+            kk, vv = kf[:, :, cols], vf[:, :, cols]
+        s = torch.matmul(q[:, :, q0:q1].float(), kk.transpose(-1, -2).contiguous()) * scale
+        ref_l = torch.logsumexp(s, -1)
+        ref = torch.matmul(torch.softmax(s, -1), vv)
+        d = (out[:, :, q0:q1].float() - ref).abs()
+        errs.append((d.max().item(), d.mean().item(), (lse[:, :, q0:q1] - ref_l).abs().max().item(),
+                     bool(torch.isfinite(out[:, :, q0:q1]).all())))
+    res = dict(rows_checked=f"{len(segs) * 64} rows (first/last 64 global, {len(picks)} ordinary "
+               "64-query rows) x all heads",
+               max_abs=float(f"{max(e[0] for e in errs):.3e}"),
+               mean_abs=float(f"{max(e[1] for e in errs):.3e}"),
+               lse_abs=float(f"{max(e[2] for e in errs):.3e}"))
+    res["ok"] = bool(all(e[3] for e in errs) and all(res[key] <= tol for key, tol in TOLERANCE.items()))
+    return res
+
+
+def config_figures(dev, stream, peak_measured, reps=10):
+    """The other BASELINE configurations in this run (reference hilberta/benchmark.py:13-22 takes
+    the shape on its command line; results csv rows 13-17, 33-37, 57, 63-67, 77, 83-87): per
+    configuration the phase-weighted ms of paired_attention, live TFLOP/s, the fraction of the
+    nominal and of the measured MFMA peak, and a sampled parity check.  Q/K/V are drawn on the
+    device from seed 2707 (as benchmark.py:24-28 does).  Also the same 2048 px 16-tile K3 call on
+    the quad (256-query) kernel and on the unpaired 64-query kernel, through the C ABI."""
+    import ctypes
+    import math
+
+    from hilberta_amd import _lib
+    from hilberta_amd._tables import quad_rows_device
+    from hilberta_amd._workspace import attention_workspace
+    from hilberta_amd.bridge_k import bridge_k_plan, paired_plan_device
+    from hilberta_amd.paired_kernel import paired_attention
+
+    lib = _lib.load()
+    cases = [("1024_t4k1", 1, "paired"), ("1024_t4k1", 4, "paired"), ("1024_t16k3", 1, "paired"),
+             ("2048_t4k1", 1, "paired"), ("4096_t16k3", 1, "paired"), ("2048_t16k3", 1, "quad"),
+             ("2048_t16k3", 1, "unpaired")]
+    figs = {}
+    for name, batch, kind in cases:
+        grid, tiles, kk = CONFIGS[name]
+        plan = paired_plan_device(tiles, kk, grid_size=grid, device=dev)
+        N, G = plan.total_tokens, plan.global_tokens
+        T = N // 64
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(2707)
+        q, k, v = (torch.randn(batch, HEADS, N, DIM, device=dev, generator=gen).to(torch.bfloat16)
+                   for _ in range(3))
+        out = torch.empty_like(q)
+        lse = torch.empty(batch, HEADS, N, dtype=torch.float32, device=dev)
+        scale_log2 = DIM ** -0.5 * 1.4426950408889634
+        strides = (ctypes.c_int64 * 12)(*[s for x in (q, k, v, out) for s in x.stride()[:3]])
+        metas = plan.phases
+        live = [live_blocks(m) for m in metas]
+
+        def c_call(fn, ids, flags, counts, paired_kind, p_lse):
+            width = ids.shape[1]
+            ws = attention_workspace(dev, batch, HEADS, N, DIM, G, width, 64, paired=paired_kind,
+                                     all_queries=1)
+            args = [q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                    p_lse.data_ptr() if p_lse is not None else None, strides, batch, HEADS, N, DIM,
+                    0, ids.data_ptr()]
+            args += [flags.data_ptr()] if flags is not None else []
+            args += [counts.data_ptr(), width, G]
+            args += [64] if fn in ("hb_paired_fwd", "hb_block_sparse_fwd") else []
+            args += [1, scale_log2, ws.data_ptr(), ws.numel(), 0, stream.cuda_stream]
+            _lib.check(getattr(lib, fn)(*args), fn)
+
+        if kind == "paired":
+            calls = [lambda m=m, l=None: paired_attention(q, k, v, m, global_strategy="triton",
+                                                          out=out, lse=l) for m in metas]
+            kernel = "attn_fwd_kernel<2,128,1,false> (hb_paired_fwd)"
+        elif kind == "quad":
+            quads = [quad_rows_device(m.kv_indices, m.kv_counts, T, kv_flags=m.kv_flags,
+                                      quad_width=min(2 * m.kv_indices.shape[1], T)) for m in metas]
+            widths = [int(c.max()) for _, _, c in quads]
+            quads = [(i[:, :w].contiguous(), f[:, :w].contiguous(), c)
+                     for (i, f, c), w in zip(quads, widths)]
+            calls = [lambda t=t, l=None: c_call("hb_quad_fwd", t[0], t[1], t[2], 2, l) for t in quads]
+            kernel = "attn_fwd_kernel<4,128,1,false> (hb_quad_fwd)"
+        else:
+            host = bridge_k_plan(tiles, kk, False, grid_size=grid)
+            tabs = [(ph.kv_indices.to(dev), ph.kv_counts.to(dev)) for ph in host.phases]
+            calls = [lambda t=t, l=None: c_call("hb_block_sparse_fwd", t[0], None, t[1], 0, l)
+                     for t in tabs]
+            kernel = "attn_fwd_kernel<1,128,1,false> (hb_block_sparse_fwd)"
+        n_reps = reps if N < 32768 else max(3, reps // 2)
+        med = []
+        for fn in calls:
+            for _ in range(2):
+                fn()
+            med.append(statistics.median(event_time(fn, n_reps, stream)))
+        weighted = sum(w * t for w, t in zip(WEIGHTS, med)) / sum(WEIGHTS)
+        flops = [4 * DIM * 64 * 64 * HEADS * batch * lb for lb in live]
+        w_flops = sum(w * f for w, f in zip(WEIGHTS, flops)) / sum(WEIGHTS)
+        tf = w_flops / (weighted * 1e-3) / 1e12
+        # sampled parity on phase 1 (every kind writes out / lse of the same call)
+        calls[1](l=lse)
+        rows = row_lists(metas[1], N, G)
+        picks = sorted({0, len(rows) - 1, *range(0, len(rows), max(1, len(rows) // 6))})
+        par = sampled_parity(out, lse, q, k, v, rows, G, DIM ** -0.5, picks)
+        label = f"{name}_b{batch}" + ("" if kind == "paired" else f"_{kind}")
+        figs[label] = dict(kernel=kernel, phase_ms=[round(x, 4) for x in med],
+                           ms=round(weighted, 4), live_tflops=round(tf, 1),
+                           mfma_util=round(tf / PEAK_BF16_TFLOPS, 4),
+                           mfma_util_vs_measured_peak=round(tf / peak_measured, 4),
+                           live_blocks=live, parity=par)
+        log(f"  config {label}: {weighted:.4f} ms, {tf:.0f} TFLOP/s, parity ok={par['ok']}")
+        del q, k, v, out, lse
+    return figs
+
+
 def cpu_table_build_ms(tiles, k, grid):
     """The oracle's numpy table build (bridge_k_plan + pair_metadata, four phases) on the host."""
     root = os.path.dirname(os.path.abspath(__file__))
@@ -443,6 +590,8 @@ def main():
                     help="seconds of CPU baseline work on the headline shape")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="attention only (for counter runs)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other configurations' figures (the `configs` block)")
     ap.add_argument("--no-parity", action="store_true",
                     help="skip the in-run parity check (for kernel-trace runs, whose per-kernel "
                     "statistics it would crowd with its own fp32 reference kernels)")
@@ -660,7 +809,11 @@ def main():
                                                 unit="GB/s", frac=round(gbps / PEAK_HBM_GBS, 4),
                                                 algorithmic_bytes=nbytes, traffic=traffic))
             del src, dst, pad
+            peak_tf, peak_ms = mfma_peak_tflops(stream)
             extras = dict(
+                mfma_peak_measured_tflops=round(peak_tf, 1),
+                mfma_peak_probe_ms=round(peak_ms, 4),
+                mfma_util_vs_measured_peak=round(achieved / peak_tf, 4),
                 stream_copy_GBps=round(2 * (1 << 30) / (copy_ms * 1e-3) / 1e9, 1),
                 dense_sdpa_ms=round(dense_sdpa, 4),
                 dense_sdpa_tflops=round(dense_flops / (dense_sdpa * 1e-3) / 1e12, 1),
@@ -769,6 +922,12 @@ def main():
         "parity": parity,
         **extras,
     }
+    if not a.no_extras and not a.no_configs:
+        log("other configurations ...")
+        with torch.inference_mode():
+            result["configs"] = config_figures(dev, stream, result["mfma_peak_measured_tflops"])
+        if not all(f["parity"]["ok"] for f in result["configs"].values()):
+            parity["ok"] = False
     if not a.no_cpu_baseline:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(plan.phases[0], q, k_, v, a.cpu_budget)

@@ -70,6 +70,7 @@ SIGNATURES = {
     "hb_bits_emit": (_c_int, [_p, _c_int, _c_int, _c_int, _p, _c_int, _p, _p, _c_int, _p]),
     "hb_pair_rows": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _p, _p]),
     "hb_quad_rows": (_c_int, [_p, _p, _p, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _p, _p]),
+    "hb_mfma_peak_probe": (_c_int, [_c_int, _c_int, _p, _p, _p]),
 }
 
 _lib = None

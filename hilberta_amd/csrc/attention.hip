@@ -207,9 +207,6 @@ __global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  // wave index as a provably uniform (scalar) value, so per-wave tests such as the flag check
-  // compile to branches rather than exec-masked code
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // Two waves share each SIMD, and with equal priorities they tend to reach the MFMA and softmax
   // phases together; a higher issue priority for one of them lets it run ahead.  With two
   // workgroups per CU the upper half of the persistent grid takes it (5-7 % faster at 2048 px
@@ -217,7 +214,11 @@ __global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, 
   // and a workgroup whose claim finds every queue drained gives it up for its last item (see
   // `step`).  An eight-wave quad workgroup holds both waves of each SIMD (waves w and w + 4
   // under round-robin placement): its upper four waves take it.
-  if (HALVES == 4 ? wave >= 4 : blockIdx.x >= gridDim.x / 2) __builtin_amdgcn_s_setprio(1);
+  if (HALVES != 4 && blockIdx.x >= gridDim.x / 2) __builtin_amdgcn_s_setprio(1);
+  // wave index as a provably uniform (scalar) value, so per-wave tests such as the flag check
+  // compile to branches rather than exec-masked code
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (HALVES == 4 && wave >= 4) __builtin_amdgcn_s_setprio(1);
   // query block (64 queries) of this wave: the flag bit it tests
   const int half = HALVES >= 2 ? (wave * QW) / 64 : 0;
   // flags of a block every query block of the item sees (global chunks)

@@ -234,6 +234,16 @@ int hb_quad_rows(const int32_t* kv_indices, const int32_t* kv_flags, const int32
                  int32_t* quad_flags, int32_t* quad_counts, int32_t quad_width, int32_t* overflow,
                  hb_stream_t stream);
 
+/* ---------------------------------------------------------------- measurement
+ * Dense bf16 MFMA peak probe: `groups` workgroups (0 = two per compute unit) of four waves, each
+ * wave issuing `iterations` x 4 independent v_mfma_f32_32x32x16_bf16 back to back; *flops (host
+ * int64) receives the floating-point operations of the launch, to be divided by its event-timed
+ * duration.  `sink` is a device float array of groups x 256 entries that the kernel never writes
+ * for its fixed operands.  No counterpart in the reference: it measures the ceiling the benchmark
+ * states its MFMA utilisation against. */
+int hb_mfma_peak_probe(int32_t iterations, int32_t groups, float* sink, int64_t* flops,
+                       hb_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
