@@ -71,6 +71,11 @@ SIGNATURES = {
     "hb_pair_rows": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _p, _p]),
     "hb_quad_rows": (_c_int, [_p, _p, _p, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _p, _p]),
     "hb_mfma_peak_probe": (_c_int, [_c_int, _c_int, _p, _p, _p]),
+    "hb_paired_plan_scratch_bytes": (_c_i64, [_c_int, _c_int]),
+    "hb_paired_plan_tables": (
+        _c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+    ),
+    "hb_paired_plan_emit": (_c_int, [_c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p, _p, _p]),
 }
 
 _lib = None

@@ -247,3 +247,57 @@ def quad_rows_device(kv_indices, kv_counts, total_blocks, *, kv_flags=None, quad
                                   _lib.stream_ptr(device))
     _lib.check(rc, "hb_quad_rows")
     return ids, flags, counts
+
+
+def paired_plan_tables_device(grid_size, tile_count, k, text_tokens, shared, key_block_size,
+                              device=None):
+    """Layout and the four phases' paired tables of bridge_k_plan + pair_metadata in six launches
+    and one host read (hb_paired_plan_tables / hb_paired_plan_emit).
+
+    Returns (DeviceLayout, [(ids, flags, counts) per phase]) on the device.  The host read takes the
+    shared-prefix length, the layout checks and the four table widths at once.
+    """
+    import ctypes
+
+    device = _dev(device)
+    lib = _lib.load()
+    n = grid_size * grid_size
+    nb = n // 64
+    orders = torch.empty(4 * n + 2 * nb, dtype=torch.int64, device=device)
+    t = [orders[i * n:(i + 1) * n] for i in range(4)]
+    t += [orders[4 * n:4 * n + nb], orders[4 * n + nb:]]
+    need = lib.hb_paired_plan_scratch_bytes(grid_size, text_tokens)
+    if need < 0:
+        raise ValueError("invalid plan geometry")
+    scratch = torch.empty(need, dtype=torch.uint8, device=device)
+    status = torch.empty(7, dtype=torch.int32, device=device)
+    stream = _lib.stream_ptr(device)
+    rc = lib.hb_paired_plan_tables(grid_size, tile_count, k, text_tokens, int(bool(shared)),
+                                   key_block_size, *[x.data_ptr() for x in t], scratch.data_ptr(),
+                                   status.data_ptr(), stream)
+    _lib.check(rc, "hb_paired_plan_tables")
+    # setup-time sync: the shared-prefix length, the layout checks and the table widths
+    n_shared, partial, bad_order, *widths = status.tolist()
+    if partial:
+        raise ValueError("Shared square must be a union of complete original blocks")
+    if bad_order:
+        raise RuntimeError("hb_paired_plan_tables produced an image order that is not a permutation")
+    layout = DeviceLayout(grid_size, 64, text_tokens, n_shared, *t)
+    nq = nb - n_shared
+    if nq % 2:
+        raise ValueError("Paired queries require N/global aligned to 128; KV must be 64/128")
+    rows = nq // 2
+    widths = [max(int(w), 1) for w in widths]
+    buf = torch.empty(sum(2 * rows * w + rows for w in widths), dtype=torch.int32, device=device)
+    tables, off = [], 0
+    for w in widths:
+        ids = buf[off:off + rows * w].view(rows, w)
+        flags = buf[off + rows * w:off + 2 * rows * w].view(rows, w)
+        counts = buf[off + 2 * rows * w:off + 2 * rows * w + rows]
+        off += 2 * rows * w + rows
+        tables.append((ids, flags, counts))
+    ptrs = lambda i: (ctypes.c_void_p * 4)(*[tb[i].data_ptr() for tb in tables])  # noqa: E731
+    rc = lib.hb_paired_plan_emit(grid_size, text_tokens, n_shared, key_block_size, scratch.data_ptr(),
+                                 ptrs(0), ptrs(1), ptrs(2), (ctypes.c_int32 * 4)(*widths), stream)
+    _lib.check(rc, "hb_paired_plan_emit")
+    return layout, tables

@@ -16,7 +16,7 @@ import torch
 
 from .paired_metadata import PairedMetadata
 from .plan import _check_geometry, _device_plan, _to_attention_plan
-from ._tables import DeviceLayout, emit_device_many, layout_device, phase_bits_device
+from ._tables import DeviceLayout, paired_plan_tables_device
 
 
 def _check_k(k):
@@ -51,20 +51,15 @@ class DevicePlan:
 
 def paired_plan_device(tiles=4, k=1, shared=False, *, grid_size=64, text_tokens=512,
                        key_block_size=64, device=None):
-    """bridge_k_plan + pair_metadata for all four phases without leaving the GPU."""
+    """bridge_k_plan + pair_metadata for all four phases without leaving the GPU: six launches and
+    one host read (_tables.paired_plan_tables_device)."""
     _check_k(k)
     tiles, grid_size, text_tokens, block_size = _check_geometry(tiles, grid_size, text_tokens, 64)
-    layout = layout_device(grid_size, block_size, text_tokens, shared, device)
+    if key_block_size not in (64, 128) or (text_tokens + grid_size**2) % 128:
+        raise ValueError("Paired queries require N/global aligned to 128; KV must be 64/128")
+    layout, tables = paired_plan_tables_device(grid_size, tiles, k, text_tokens, shared,
+                                               key_block_size, device)
     N = text_tokens + grid_size**2
     G = layout.global_blocks * block_size
-    if N % 128 or G % 128 or key_block_size not in (64, 128):
-        raise ValueError("Paired queries require N/global aligned to 128; KV must be 64/128")
-    scratch = torch.empty(layout.image_blocks**2, dtype=torch.int32, device=layout.original_order.device)
-    # The four phases' launches queue back to back (the score scratch is reused in stream order)
-    # with one host read of their table widths.
-    bits = [phase_bits_device(layout, tiles, phase, 2, k, scratch)[0] for phase in range(4)]
-    tables = emit_device_many(bits, layout.total_blocks, unpaired=False, paired=True,
-                              key_block_size=key_block_size)
-    metas = [PairedMetadata(t["paired_indices"], t["paired_flags"], t["paired_counts"], N, G,
-                            key_block_size) for t in tables]
+    metas = [PairedMetadata(ids, flags, counts, N, G, key_block_size) for ids, flags, counts in tables]
     return DevicePlan(layout, tiles, k, metas)

@@ -656,3 +656,367 @@ extern "C" int hb_quad_rows(const int32_t* kv_indices, const int32_t* kv_flags,
   HB_HIP(hipGetLastError());
   return HB_OK;
 }
+
+// ---------------------------------------------------------------------------------------------
+// Fused device plan (bridge_k_plan + pair_metadata for all four phases, reciprocal top-K bridges,
+// paired_plan_device): six launches and one host read instead of one launch sequence per phase.
+// The global-prefix length (the shared blocks of the layout) stays on the device: the phase
+// kernels read it from status[0], so nothing synchronises before the table widths are known.
+//
+//   P1 composite order (grid-wide) + clearing the four phases' score matrices
+//   P2 one workgroup: block packing, image order and its inverse, the permutation check, status
+//   P3 bridge scores of all four phases (atomic adds per raster 4-neighbour pair) + base rows
+//   P4 top-K per (phase, query block), reciprocal bridge bits
+//   P5 paired row counts per phase -> status[3 + phase] = widest row
+//   -- host reads status (n_shared, partial, bad order, four widths), allocates exact tables --
+//   P6 emit the four phases' paired ids / flags / counts at their exact widths
+//
+// Scratch: 4 nb^2 int32 scores, then 4 x nb x words uint32 bitmaps (rows = ordinary blocks, of
+// which the first T - gb are used).  status: int32[7].
+namespace {
+
+constexpr int PLAN_PHASES = 4;
+
+__global__ void plan_composite_kernel(int g, int64_t* original, int64_t* inverse, int32_t* scores,
+                                      int64_t score_words) {
+  const int64_t n = (int64_t)g * g;
+  const int64_t total = n > score_words ? n : score_words;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    if (i < n) {
+      const int64_t half = n / 2;
+      const int64_t src = n / 4 + (i < half ? i : i - half);
+      const int64_t h = hilbert_raster(src, g);
+      const int64_t tok = i < half ? h : n - 1 - h;
+      original[i] = tok;
+      inverse[tok] = i;
+    }
+    if (i < score_words) scores[i] = 0;
+  }
+}
+
+// The block packing of pack_blocks_kernel, then (same workgroup, after a barrier) the image order,
+// its inverse and the permutation check of image_order_kernel / order_check_kernel.
+__global__ void __launch_bounds__(1024) plan_pack_kernel(int g, int bs, int shared,
+                                                         const int64_t* original, int text_blocks,
+                                                         int64_t* packed, int64_t* to_physical,
+                                                         int64_t* order, int64_t* inverse_order,
+                                                         int32_t* status) {
+  const int64_t n = (int64_t)g * g;
+  const int nb = (int)(n / bs);
+  __shared__ int s_total[3];
+  __shared__ int s_scan[1024];
+  const int t = threadIdx.x;
+  const int per = (nb + 1023) / 1024;
+  const int lo = min(t * per, nb), hi = min(lo + per, nb);
+  const int start = 3 * g / 8, end = 5 * g / 8;
+  auto shared_tokens = [&](int b) {
+    int cnt = 0;
+    if (shared) {
+      for (int j = 0; j < bs; ++j) {
+        const int64_t tok = original[(int64_t)b * bs + j];
+        const int y = (int)(tok / g), x = (int)(tok % g);
+        cnt += (y >= start && y < end && x >= start && x < end);
+      }
+    }
+    return cnt;
+  };
+  int my_shared = 0, partial = 0;
+  for (int b = lo; b < hi; ++b) {
+    const int cnt = shared_tokens(b);
+    if (cnt != 0 && cnt != bs) partial = 1;
+    my_shared += (cnt == bs);
+  }
+  s_scan[t] = my_shared;
+  if (t == 0) {
+    s_total[1] = 0;
+    s_total[2] = 0;
+  }
+  __syncthreads();
+  if (partial) atomicOr(&s_total[1], 1);
+  for (int off = 1; off < 1024; off *= 2) {
+    const int v = t >= off ? s_scan[t - off] : 0;
+    __syncthreads();
+    s_scan[t] += v;
+    __syncthreads();
+  }
+  const int n_shared = s_scan[1023];
+  int sh_before = s_scan[t] - my_shared;
+  int ord_before = lo - sh_before;
+  for (int b = lo; b < hi; ++b) {
+    const int slot = shared_tokens(b) == bs ? sh_before++ : n_shared + ord_before++;
+    packed[slot] = b;
+    to_physical[b] = slot + text_blocks;
+  }
+  __syncthreads();  // packed complete (global writes of this workgroup are visible after it)
+  for (int64_t i = t; i < n; i += 1024) {
+    const int64_t tok = original[packed[i / bs] * bs + i % bs];
+    order[i] = tok;
+    if (tok >= 0 && tok < n) inverse_order[tok] = i;
+  }
+  __syncthreads();
+  int bad = 0;
+  for (int64_t i = t; i < n; i += 1024) {
+    const int64_t tok = order[i];
+    bad |= tok < 0 || tok >= n || inverse_order[tok] != i;
+  }
+  if (bad) atomicOr(&s_total[2], 1);
+  __syncthreads();
+  if (t == 0) {
+    status[0] = n_shared;
+    status[1] = s_total[1];
+    status[2] = s_total[2];
+  }
+  if (t < PLAN_PHASES) status[3 + t] = 0;
+}
+
+// Bridge scores of the four phases (blocks [0, score_blocks)) and their base rows (the rest).
+__global__ void plan_scores_base_kernel(int g, int bs, int tiles, int text_blocks, int score_blocks,
+                                        const int64_t* inverse, const int64_t* packed,
+                                        const int32_t* status, int32_t* scores, uint32_t* bits) {
+  const int64_t n = (int64_t)g * g;
+  const int nb = (int)(n / bs);
+  const int T = text_blocks + nb;
+  const int words = (T + 31) / 32;
+  const int64_t width = n / tiles;
+  if ((int)blockIdx.x < score_blocks) {
+    const int64_t pairs = 2 * (int64_t)g * (g - 1);
+    for (int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; p < pairs; p += (int64_t)score_blocks * blockDim.x) {
+      int64_t a, c;
+      if (p < (int64_t)g * (g - 1)) {
+        const int64_t y = p / (g - 1), x = p % (g - 1);
+        a = y * g + x;
+        c = a + 1;
+      } else {
+        const int64_t q = p - (int64_t)g * (g - 1);
+        a = q;
+        c = q + g;
+      }
+      const int64_t pa = inverse[a], pc = inverse[c];
+      const int ba = (int)(pa / bs), bc = (int)(pc / bs);
+      for (int ph = 0; ph < PLAN_PHASES; ++ph) {
+        const int64_t off = ph * (width / 4);
+        if (tile_label(pa, off, n, width) != tile_label(pc, off, n, width)) {
+          int32_t* sc = scores + (int64_t)ph * nb * nb;
+          atomicAdd(&sc[(int64_t)ba * nb + bc], 1);
+          atomicAdd(&sc[(int64_t)bc * nb + ba], 1);
+        }
+      }
+    }
+    return;
+  }
+  // base rows (plan.py:173-183): one lane per (phase, row, key block), as base_bits_kernel
+  const int gb = text_blocks + status[0];
+  const int nq = T - gb;
+  const int spans = (T + 63) / 64;
+  const int64_t total = (int64_t)PLAN_PHASES * nb * spans * 64;
+  const int lane = threadIdx.x & 63;
+  const int64_t first = (blockIdx.x - score_blocks) * (int64_t)blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)(gridDim.x - score_blocks) * blockDim.x;
+  for (int64_t idx = first; idx < total; idx += stride) {
+    const int64_t span = idx >> 6;
+    const int ph = (int)(span / ((int64_t)nb * spans));
+    const int64_t rs = span - (int64_t)ph * nb * spans;
+    const int r = (int)(rs / spans), sp = (int)(rs % spans);
+    if (r >= nq) continue;  // whole wave: a span belongs to one row
+    const int64_t off = ph * (width / 4);
+    const int p = sp * 64 + lane;
+    bool on = false;
+    if (p < gb) {
+      on = true;
+    } else if (p < T) {
+      const int lab = tile_label(packed[gb - text_blocks + r] * bs, off, n, width);
+      on = tile_label(packed[p - text_blocks] * bs, off, n, width) == lab;
+    }
+    const uint64_t m = __ballot(on);
+    const int w = sp * 2 + (lane >> 5);
+    if ((lane & 31) == 0 && w < words)
+      bits[((int64_t)ph * nb + r) * words + w] = (uint32_t)(m >> (lane & 32));
+  }
+}
+
+// Top-K per (phase, original query block) as topk_kernel, then the reciprocal bridge bits of its
+// picks as bridge_bits_kernel (adj | adj^T, bridge_k.py:36-44).
+__global__ void plan_topk_bits_kernel(int g, int bs, int tiles, int k, int text_blocks,
+                                      const int32_t* scores, const int64_t* to_physical,
+                                      const int32_t* status, uint32_t* bits) {
+  const int64_t n = (int64_t)g * g;
+  const int nb = (int)(n / bs);
+  const int T = text_blocks + nb;
+  const int words = (T + 31) / 32;
+  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (wave >= PLAN_PHASES * nb) return;
+  const int ph = wave / nb, q = wave - ph * nb;
+  const int offset_blocks = (int)(ph * (n / tiles / 4) / bs);
+  const int32_t* sc = scores + (int64_t)ph * nb * nb + (int64_t)q * nb;
+  const int gb = text_blocks + status[0];
+  uint32_t* pb = bits + (int64_t)ph * nb * words;
+  const int pq = (int)to_physical[q];
+  uint64_t bound = ~0ull;
+  for (int j = 0; j < k; ++j) {
+    uint64_t best = 0;
+    for (int key = lane; key < nb; key += 64) {
+      const int s = sc[key];
+      if (s <= 0) continue;
+      const int rolled = ((key - offset_blocks) % nb + nb) % nb;
+      const uint64_t code = ((uint64_t)(uint32_t)s << 32) | (uint32_t)(nb - 1 - rolled);
+      if (code < bound && code > best) best = code;
+    }
+    best = wave_max_u64(best);
+    if (!best) break;
+    if (lane == 0) {
+      const int rolled = nb - 1 - (int)(best & 0xffffffffu);
+      const int key = (rolled + offset_blocks) % nb;
+      const int pk = (int)to_physical[key];
+      if (pq >= gb) atomicOr(&pb[(int64_t)(pq - gb) * words + pk / 32], 1u << (pk % 32));
+      if (pk >= gb) atomicOr(&pb[(int64_t)(pk - gb) * words + pq / 32], 1u << (pq % 32));
+    }
+    bound = best;
+  }
+}
+
+// Paired counts of the four phases: one wave per (phase, paired row); the widest row of each
+// phase goes to status[3 + phase].
+__global__ void plan_counts_kernel(int nb, int words, int T, int text_blocks, int ratio,
+                                   const uint32_t* bits, int32_t* status) {
+  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  const int prows_max = nb / 2;
+  if (wave >= PLAN_PHASES * prows_max) return;
+  const int ph = wave / prows_max, pr = wave - ph * prows_max;
+  const int nq = T - text_blocks - status[0];
+  if (pr >= nq / 2) return;  // (an odd nq is rejected on the host)
+  const uint32_t* ra = bits + ((int64_t)ph * nb + 2 * pr) * words;
+  const uint32_t* rb = ra + words;
+  const int kblocks = (T + ratio - 1) / ratio;
+  int c = 0;
+  for (int kb = lane; kb < kblocks; kb += 64) c += pair_flag(ra, rb, kb, ratio) != 0;
+  for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off);
+  if (lane == 0) atomicMax(&status[3 + ph], c);
+}
+
+struct PlanOut {
+  int32_t* ids[PLAN_PHASES];
+  int32_t* flags[PLAN_PHASES];
+  int32_t* counts[PLAN_PHASES];
+  int32_t width[PLAN_PHASES];
+};
+
+// Paired tables of the four phases at their exact widths (emit_kernel, mode 1).
+__global__ void plan_emit_kernel(int nb, int words, int T, int prows, int ratio,
+                                 const uint32_t* bits, PlanOut out) {
+  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (wave >= PLAN_PHASES * prows) return;
+  const int ph = wave / prows, row = wave - ph * prows;
+  const uint32_t* ra = bits + ((int64_t)ph * nb + 2 * row) * words;
+  const uint32_t* rb = ra + words;
+  const int kblocks = (T + ratio - 1) / ratio;
+  const int width = out.width[ph];
+  int32_t* ids = out.ids[ph] + (int64_t)row * width;
+  int32_t* fl = out.flags[ph] + (int64_t)row * width;
+  int base = 0;
+  for (int k0 = 0; k0 < kblocks; k0 += 64) {
+    const int kb = k0 + lane;
+    const int flag = kb < kblocks ? pair_flag(ra, rb, kb, ratio) : 0;
+    const uint64_t ballot = __ballot(flag != 0);
+    const int pos = base + __popcll(ballot & ((1ull << lane) - 1ull));
+    if (flag && pos < width) {
+      ids[pos] = kb;
+      fl[pos] = flag;
+    }
+    base += __popcll(ballot);
+  }
+  for (int e = base + lane; e < width; e += 64) {
+    ids[e] = 0;
+    fl[e] = 0;
+  }
+  if (lane == 0) out.counts[ph][row] = base < width ? base : width;
+}
+
+}  // namespace
+
+extern "C" int64_t hb_paired_plan_scratch_bytes(int32_t grid_size, int32_t text_tokens) {
+  if (grid_size < 8 || text_tokens < 0 || text_tokens % 64) return -1;
+  const int64_t nb = (int64_t)grid_size * grid_size / 64;
+  const int64_t words = (text_tokens / 64 + nb + 31) / 32;
+  return PLAN_PHASES * (nb * nb * 4 + nb * words * 4);
+}
+
+extern "C" int hb_paired_plan_tables(int32_t grid_size, int32_t tile_count, int32_t k,
+                                     int32_t text_tokens, int32_t shared, int32_t key_block_size,
+                                     int64_t* original_order, int64_t* inverse_original,
+                                     int64_t* image_order, int64_t* inverse_image_order,
+                                     int64_t* physical_original_blocks,
+                                     int64_t* original_to_physical, void* scratch,
+                                     int32_t* status, hb_stream_t stream) {
+  HB_REQUIRE(grid_size >= 8 && (grid_size & (grid_size - 1)) == 0,
+             "grid_size must be a power of two >= 8");
+  const int64_t n = (int64_t)grid_size * grid_size;
+  HB_REQUIRE(tile_count > 0 && n % tile_count == 0 && (n / tile_count) % (4 * 64) == 0 &&
+                 text_tokens > 0 && text_tokens % 64 == 0,
+             "Tile quarter offsets and text prefix must be block aligned");
+  HB_REQUIRE(k >= 1 && k <= 4, "bridge K must be 1..4");
+  HB_REQUIRE(key_block_size == 64 || key_block_size == 128, "key_block_size must be 64 or 128");
+  HB_REQUIRE(n / 64 <= (1 << 14), "at most 16384 image blocks");
+  HB_REQUIRE(original_order && inverse_original && image_order && inverse_image_order &&
+                 physical_original_blocks && original_to_physical && scratch && status,
+             "null pointer argument");
+  const int bs = 64;
+  const int nb = (int)(n / bs), text_blocks = text_tokens / bs, T = text_blocks + nb;
+  const int words = (T + 31) / 32;
+  int32_t* scores = (int32_t*)scratch;
+  uint32_t* bits = (uint32_t*)(scores + (int64_t)PLAN_PHASES * nb * nb);
+  const int64_t score_words = (int64_t)PLAN_PHASES * nb * nb;
+  hipLaunchKernelGGL(plan_composite_kernel, dim3(grid_for(n > score_words ? n : score_words)),
+                     dim3(TPB), 0, stream, grid_size, original_order, inverse_original, scores,
+                     score_words);
+  hipLaunchKernelGGL(plan_pack_kernel, dim3(1), dim3(1024), 0, stream, grid_size, bs, shared,
+                     (const int64_t*)original_order, text_blocks, physical_original_blocks,
+                     original_to_physical, image_order, inverse_image_order, status);
+  const int score_blocks = grid_for(2 * n);
+  const int base_blocks = grid_for((int64_t)PLAN_PHASES * nb * ((T + 63) / 64) * 64);
+  hipLaunchKernelGGL(plan_scores_base_kernel, dim3(score_blocks + base_blocks), dim3(TPB), 0,
+                     stream, grid_size, bs, tile_count, text_blocks, score_blocks,
+                     (const int64_t*)inverse_original, (const int64_t*)physical_original_blocks,
+                     (const int32_t*)status, scores, bits);
+  hipLaunchKernelGGL(plan_topk_bits_kernel, dim3(((int64_t)PLAN_PHASES * nb * 64 + TPB - 1) / TPB),
+                     dim3(TPB), 0, stream, grid_size, bs, tile_count, k, text_blocks,
+                     (const int32_t*)scores, (const int64_t*)original_to_physical,
+                     (const int32_t*)status, bits);
+  hipLaunchKernelGGL(plan_counts_kernel, dim3(((int64_t)PLAN_PHASES * (nb / 2) * 64 + TPB - 1) / TPB),
+                     dim3(TPB), 0, stream, nb, words, T, text_blocks, key_block_size / 64,
+                     (const uint32_t*)bits, status);
+  HB_HIP(hipGetLastError());
+  return HB_OK;
+}
+
+extern "C" int hb_paired_plan_emit(int32_t grid_size, int32_t text_tokens, int32_t shared_blocks,
+                                   int32_t key_block_size, const void* scratch,
+                                   int32_t* const* ids, int32_t* const* flags,
+                                   int32_t* const* counts, const int32_t* widths,
+                                   hb_stream_t stream) {
+  HB_REQUIRE(grid_size >= 8 && text_tokens > 0 && text_tokens % 64 == 0, "invalid plan geometry");
+  HB_REQUIRE(key_block_size == 64 || key_block_size == 128, "key_block_size must be 64 or 128");
+  HB_REQUIRE(scratch && ids && flags && counts && widths, "null pointer argument");
+  const int64_t n = (int64_t)grid_size * grid_size;
+  const int nb = (int)(n / 64), text_blocks = text_tokens / 64, T = text_blocks + nb;
+  HB_REQUIRE(shared_blocks >= 0 && shared_blocks < nb, "shared_blocks out of range");
+  const int nq = nb - shared_blocks;
+  HB_REQUIRE(nq % 2 == 0, "paired rows need an even number of ordinary blocks");
+  PlanOut out;
+  for (int p = 0; p < PLAN_PHASES; ++p) {
+    HB_REQUIRE(ids[p] && flags[p] && counts[p] && widths[p] > 0, "phase %d: null table or width", p);
+    out.ids[p] = ids[p];
+    out.flags[p] = flags[p];
+    out.counts[p] = counts[p];
+    out.width[p] = widths[p];
+  }
+  const int words = (T + 31) / 32;
+  const uint32_t* bits = (const uint32_t*)((const int32_t*)scratch + (int64_t)PLAN_PHASES * nb * nb);
+  const int prows = nq / 2;
+  hipLaunchKernelGGL(plan_emit_kernel, dim3(((int64_t)PLAN_PHASES * prows * 64 + TPB - 1) / TPB),
+                     dim3(TPB), 0, stream, nb, words, T, prows, key_block_size / 64, bits, out);
+  HB_HIP(hipGetLastError());
+  return HB_OK;
+}

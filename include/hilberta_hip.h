@@ -220,6 +220,27 @@ int hb_pair_rows(const int32_t* kv_indices, const int32_t* kv_counts, int32_t ro
                  int32_t* paired_flags, int32_t* paired_counts, int32_t paired_width,
                  int32_t* overflow, hb_stream_t stream);
 
+/* Fused device plan: bridge_k_plan(tiles, K, shared, grid_size) + pair_metadata for all four
+ * phases (reference hilberta/bridge_k.py:10-51, plan.py:133-197, paired_metadata.py:26-51), in
+ * two calls with one host read between them.  hb_paired_plan_tables fills the layout (int64 [n]
+ * orders, int64 [n/64] block maps, as hb_plan_layout) and, in `scratch`
+ * (hb_paired_plan_scratch_bytes), the four phases' adjacency bitmaps, and writes status (device
+ * int32[7]) = {#shared blocks, partial-shared-block flag, 1 if the image order is not a
+ * permutation, widest paired row of phases 0..3}.  After reading status the caller allocates
+ * each phase's paired tables ([(nb - shared)/2, width]) and calls hb_paired_plan_emit with host
+ * arrays of the four device pointers and widths.  64-token blocks; at most 16384 image blocks. */
+int64_t hb_paired_plan_scratch_bytes(int32_t grid_size, int32_t text_tokens);
+int hb_paired_plan_tables(int32_t grid_size, int32_t tile_count, int32_t k, int32_t text_tokens,
+                          int32_t shared, int32_t key_block_size, int64_t* original_order,
+                          int64_t* inverse_original, int64_t* image_order,
+                          int64_t* inverse_image_order, int64_t* physical_original_blocks,
+                          int64_t* original_to_physical, void* scratch, int32_t* status,
+                          hb_stream_t stream);
+int hb_paired_plan_emit(int32_t grid_size, int32_t text_tokens, int32_t shared_blocks,
+                        int32_t key_block_size, const void* scratch, int32_t* const* ids,
+                        int32_t* const* flags, int32_t* const* counts, const int32_t* widths,
+                        hb_stream_t stream);
+
 /* Quad tables for hb_quad_fwd in one launch.  With kv_flags: kv_indices/kv_flags/kv_counts are
  * paired 64-key tables ([rows, width], rows even; pair_metadata's output, reference
  * hilberta/paired_metadata.py:26-51) and quad row r is the union of paired rows 2r and 2r + 1,

@@ -104,19 +104,30 @@ def test_pair_metadata_bit_exact(hip_device, name, grid, tiles, k, key_block):
             _eq(getattr(meta, f), ref[f], f"{name} phase {phase} {f}")
 
 
-@pytest.mark.parametrize("grid,tiles,k", [(64, 4, 1), (128, 16, 3), (256, 16, 3)])
-def test_paired_plan_device_bit_exact(hip_device, grid, tiles, k):
+@pytest.mark.parametrize("grid,tiles,k,shared,key_block", [
+    (64, 4, 1, False, 64), (64, 16, 2, False, 64), (64, 4, 4, False, 128), (64, 16, 3, True, 64),
+    (128, 4, 1, False, 64), (128, 16, 3, False, 64), (128, 16, 3, False, 128), (128, 4, 2, True, 64),
+    (256, 16, 3, False, 64), (256, 4, 1, False, 64)])
+def test_paired_plan_device_bit_exact(hip_device, grid, tiles, k, shared, key_block):
+    """The fused device plan (six launches, one host read) against the oracle: every layout array
+    and the four phases' paired tables, widths and zero padding included."""
     from hilberta_amd.bridge_k import paired_plan_device
 
-    dp = paired_plan_device(tiles, k, grid_size=grid, device=hip_device)
-    ref_plan = T.bridge_k_plan(tiles, k, False, grid_size=grid)
-    _eq(dp.layout.image_order, ref_plan["image_order"], "image_order")
+    say(f"case paired_plan_device grid={grid} tiles={tiles} K={k} shared={shared} KB{key_block}")
+    dp = paired_plan_device(tiles, k, shared, grid_size=grid, key_block_size=key_block,
+                            device=hip_device)
+    ref_plan = T.bridge_k_plan(tiles, k, shared, grid_size=grid)
+    for f in ("image_order", "inverse_image_order", "original_order", "physical_original_blocks"):
+        _eq(getattr(dp.layout, f), ref_plan[f], f)
+    assert dp.global_tokens == ref_plan["global_tokens"]
     for phase, meta in enumerate(dp.phases):
         p = ref_plan["phases"][phase]
         ref = T.pair_metadata(p["kv_indices"], p["kv_counts"], tokens=ref_plan["total_tokens"],
-                              global_tokens=ref_plan["global_tokens"])
-        assert meta.tokens == ref_plan["total_tokens"] and meta.global_tokens == 512
+                              global_tokens=ref_plan["global_tokens"], key_block_size=key_block)
+        assert meta.tokens == ref_plan["total_tokens"]
+        assert meta.global_tokens == ref_plan["global_tokens"]
         for f in ("kv_indices", "kv_flags", "kv_counts"):
+            assert getattr(meta, f).is_contiguous()
             _eq(getattr(meta, f), ref[f], f"device plan phase {phase} {f}")
 
 
