@@ -140,13 +140,6 @@ def stream_ptr(device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def capture_id(stream: int) -> int:
-    """Identifier of the graph capture the raw hipStream_t ``stream`` takes part in, 0 if none."""
-    out = ctypes.c_uint64(0)
-    check(load().hb_stream_capture_id(stream, ctypes.byref(out)), "hb_stream_capture_id")
-    return out.value
-
-
 def require_gpu(*tensors) -> None:
     for t in tensors:
         if not (isinstance(t, torch.Tensor) and t.is_cuda):

@@ -1,11 +1,14 @@
-"""Per-(device, stream, graph capture) workspaces for the attention kernels.
+"""Per-(device, stream) workspaces for the attention kernels.
 
 A workspace holds the persistent kernel's work-queue counters (zero-filled once at allocation;
 every launch leaves them at zero) and the partial results of split global query tiles.  Keying
-by stream keeps launches that may overlap in time from sharing one; launches captured into a HIP
-graph get a workspace per capture (graphs captured one after another on the same stream may be
-replayed concurrently later), made during the capture, so every replay zero-fills it first, and
-kept for the life of the process since the graph may be replayed at any time.
+by stream keeps launches that may overlap in time from sharing one.
+
+A launch captured into a HIP graph gets a workspace of its own, made during the capture with a
+fill kernel (so every replay zero-fills it before the attention kernel runs) and released when the
+launch returns: it comes from the capture's private memory pool, which the graph keeps alive, and
+later allocations of the same capture may reuse it only in stream order, after this launch's
+kernels.  Captured launches therefore hold no memory beyond their graph's lifetime.
 """
 
 from __future__ import annotations
@@ -15,8 +18,6 @@ import torch
 from . import _lib
 
 _CACHE: dict = {}
-# every workspace a captured launch uses: graphs keep pointing at them after the cache moves on
-_CAPTURED: list = []
 
 
 def attention_workspace(device, batch, heads, tokens, head_dim, global_tokens, width,
@@ -26,18 +27,17 @@ def attention_workspace(device, batch, heads, tokens, head_dim, global_tokens, w
         int(all_queries))
     if need < 0:
         _lib.check(1, "hb_attention_workspace_bytes")
+    if torch.cuda.is_current_stream_capturing():
+        return torch.zeros(max(need, 1 << 16), dtype=torch.uint8, device=device)
     stream = torch.cuda.current_stream(device)
-    capture = _lib.capture_id(stream.cuda_stream) if torch.cuda.is_current_stream_capturing() else 0
-    key = (str(device), stream.cuda_stream, capture)
+    key = (str(device), stream.cuda_stream)
     ws = _CACHE.get(key)
     if ws is None or ws.numel() < need:
         ws = torch.zeros(max(need, 1 << 16), dtype=torch.uint8, device=device)
         _CACHE[key] = ws
-        if capture:
-            _CAPTURED.append(ws)
     return ws
 
 
 def clear() -> None:
-    """Drop the cached eager workspaces (those of captured graphs stay alive)."""
+    """Drop the cached eager workspaces."""
     _CACHE.clear()

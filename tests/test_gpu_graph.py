@@ -83,7 +83,8 @@ def test_paired_step_graph_replays_match_eager(hip_device):
 
 def test_two_graphs_on_one_capture_stream_replay_concurrently(hip_device):
     """Graphs captured one after another on torch's shared capture stream get workspaces of
-    their own, so replaying them at the same time on two streams gives each its eager result."""
+    their own (each from its graph's private pool, none from the eager cache), so replaying them
+    at the same time on two streams gives each its eager result."""
     from hilberta_amd import _workspace
     from hilberta_amd.paired_kernel import paired_attention
 
@@ -107,8 +108,7 @@ def test_two_graphs_on_one_capture_stream_replay_concurrently(hip_device):
         with torch.cuda.graph(g):
             paired_attention(q, k, v, m, out=o)
     torch.cuda.synchronize()
-    new = [key for key in _workspace._CACHE if key not in before]
-    assert len(new) == 2 and new[0][1] == new[1][1] and new[0][2] != new[1][2] != 0
+    assert set(_workspace._CACHE) == before  # captured launches leave the eager cache alone
     streams = [torch.cuda.Stream(), torch.cuda.Stream()]
     for rep in range(4):
         say(f"case concurrent replay {rep}")
@@ -121,3 +121,43 @@ def test_two_graphs_on_one_capture_stream_replay_concurrently(hip_device):
         torch.cuda.synchronize()
         for p in range(2):
             assert torch.equal(outs[p], eager[p]), f"replay {rep} graph {p}"
+
+
+def test_captures_hold_no_memory_after_their_graphs(hip_device):
+    """A captured launch's workspace lives in its graph's private pool: capturing and dropping
+    graphs repeatedly leaves the allocated memory where it started."""
+    import gc
+
+    from hilberta_amd.paired_kernel import paired_attention
+
+    plan = oracle_plan("1024_t16k3")
+    N = plan["total_tokens"]
+    q, k, v = (x.to(hip_device) for x in A.seeded_qkv(1, 4, N, 128, seed=33))
+    meta = device_paired(oracle_paired(plan, 0), hip_device)
+    out = torch.empty_like(q)
+    ref = paired_attention(q, k, v, meta)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+
+    def capture_once():
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            paired_attention(q, k, v, meta, out=out)
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            paired_attention(q, k, v, meta, out=out)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        del g
+        gc.collect()
+        torch.cuda.synchronize()
+
+    say("case graph: repeated capture and release")
+    capture_once()
+    before = torch.cuda.memory_allocated(hip_device)
+    for _ in range(4):
+        capture_once()
+    assert torch.cuda.memory_allocated(hip_device) == before
