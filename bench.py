@@ -54,8 +54,11 @@ WEIGHTS = (15, 14, 14, 14)
 KERNEL_NAMES = {"paired": "attn_fwd_kernel<2,128,1,false> (hb_paired_fwd)",
                 "paired128": "attn_fwd_kernel<2,128,2,false> (hb_paired_fwd)",
                 # pairable 64-query tables: pair_rows_kernel (hb_pair_rows) + the paired kernel
-                "unpaired": "attn_fwd_kernel<2,128,1,false> (hb_pair_rows + hb_paired_fwd)"}
-TABLE_NAMES = {"paired": "paired", "paired128": "paired KV128", "unpaired": "unpaired (sparse_attention)"}
+                "unpaired": "attn_fwd_kernel<2,128,1,false> (hb_pair_rows + hb_paired_fwd)",
+                "quad": "attn_fwd_kernel<4,128,1,false> (hb_quad_fwd)",
+                "unpaired64": "attn_fwd_kernel<1,128,1,false> (hb_block_sparse_fwd)"}
+TABLE_NAMES = {"paired": "paired", "paired128": "paired KV128", "unpaired": "unpaired (sparse_attention)",
+               "quad": "quad (256-query rows)", "unpaired64": "unpaired, 64-query kernel"}
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 
@@ -417,6 +420,41 @@ def denoiser_bench(a):
     print(json.dumps(result), flush=True)
 
 
+def abi_attention(fn, q, k, v, out, lse, ids, flags, counts, G, stream):
+    """One attention launch straight through the C ABI: hb_quad_fwd (quad tables),
+    hb_block_sparse_fwd (unpaired 64-query tables, flags None) or hb_paired_fwd, on `stream`,
+    with the library's cached workspace for the call's shapes."""
+    import ctypes
+
+    from hilberta_amd import _lib
+    from hilberta_amd._workspace import attention_workspace
+
+    lib = _lib.load()
+    B, H, N, D = q.shape
+    width = ids.shape[1]
+    kind = {"hb_quad_fwd": 2, "hb_block_sparse_fwd": 0, "hb_paired_fwd": 1}[fn]
+    ws = attention_workspace(q.device, B, H, N, D, G, width, 64, paired=kind, all_queries=1)
+    strides = (ctypes.c_int64 * 12)(*[s for x in (q, k, v, out) for s in x.stride()[:3]])
+    args = [q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            lse.data_ptr() if lse is not None else None, strides, B, H, N, D,
+            1 if q.dtype == torch.float16 else 0, ids.data_ptr()]
+    args += [flags.data_ptr()] if flags is not None else []
+    args += [counts.data_ptr(), width, G]
+    args += [64] if kind != 2 else []
+    args += [1, D ** -0.5 * 1.4426950408889634, ws.data_ptr(), ws.numel(), 0, stream.cuda_stream]
+    _lib.check(getattr(lib, fn)(*args), fn)
+
+
+def quad_tables(metas, T):
+    """Quad (256-query) tables of paired 64-key tables, at their exact widths (one host read)."""
+    from hilberta_amd._tables import quad_rows_device
+
+    quads = [quad_rows_device(m.kv_indices, m.kv_counts, T, kv_flags=m.kv_flags,
+                              quad_width=min(2 * m.kv_indices.shape[1], T)) for m in metas]
+    widths = torch.stack([c.max() for _, _, c in quads]).tolist()
+    return [(i[:, :w].contiguous(), f[:, :w].contiguous(), c) for (i, f, c), w in zip(quads, widths)]
+
+
 def mfma_peak_tflops(stream, reps=5):
     """Dense bf16 MFMA rate this GPU sustains now: hb_mfma_peak_probe (back-to-back
     v_mfma_f32_32x32x16_bf16 on every SIMD, about a millisecond per launch), median of `reps`
@@ -477,16 +515,9 @@ def config_figures(dev, stream, peak_measured, reps=10):
     nominal and of the measured MFMA peak, and a sampled parity check.  Q/K/V are drawn on the
     device from seed 2707 (as benchmark.py:24-28 does).  Also the same 2048 px 16-tile K3 call on
     the quad (256-query) kernel and on the unpaired 64-query kernel, through the C ABI."""
-    import ctypes
-    import math
-
-    from hilberta_amd import _lib
-    from hilberta_amd._tables import quad_rows_device
-    from hilberta_amd._workspace import attention_workspace
     from hilberta_amd.bridge_k import bridge_k_plan, paired_plan_device
     from hilberta_amd.paired_kernel import paired_attention
 
-    lib = _lib.load()
     cases = [("1024_t4k1", 1, "paired"), ("1024_t4k1", 4, "paired"), ("1024_t16k3", 1, "paired"),
              ("2048_t4k1", 1, "paired"), ("4096_t16k3", 1, "paired"), ("2048_t16k3", 1, "quad"),
              ("2048_t16k3", 1, "unpaired")]
@@ -502,42 +533,20 @@ def config_figures(dev, stream, peak_measured, reps=10):
                    for _ in range(3))
         out = torch.empty_like(q)
         lse = torch.empty(batch, HEADS, N, dtype=torch.float32, device=dev)
-        scale_log2 = DIM ** -0.5 * 1.4426950408889634
-        strides = (ctypes.c_int64 * 12)(*[s for x in (q, k, v, out) for s in x.stride()[:3]])
         metas = plan.phases
         live = [live_blocks(m) for m in metas]
-
-        def c_call(fn, ids, flags, counts, paired_kind, p_lse):
-            width = ids.shape[1]
-            ws = attention_workspace(dev, batch, HEADS, N, DIM, G, width, 64, paired=paired_kind,
-                                     all_queries=1)
-            args = [q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                    p_lse.data_ptr() if p_lse is not None else None, strides, batch, HEADS, N, DIM,
-                    0, ids.data_ptr()]
-            args += [flags.data_ptr()] if flags is not None else []
-            args += [counts.data_ptr(), width, G]
-            args += [64] if fn in ("hb_paired_fwd", "hb_block_sparse_fwd") else []
-            args += [1, scale_log2, ws.data_ptr(), ws.numel(), 0, stream.cuda_stream]
-            _lib.check(getattr(lib, fn)(*args), fn)
-
         if kind == "paired":
             calls = [lambda m=m, l=None: paired_attention(q, k, v, m, global_strategy="triton",
                                                           out=out, lse=l) for m in metas]
-            kernel = "attn_fwd_kernel<2,128,1,false> (hb_paired_fwd)"
         elif kind == "quad":
-            quads = [quad_rows_device(m.kv_indices, m.kv_counts, T, kv_flags=m.kv_flags,
-                                      quad_width=min(2 * m.kv_indices.shape[1], T)) for m in metas]
-            widths = [int(c.max()) for _, _, c in quads]
-            quads = [(i[:, :w].contiguous(), f[:, :w].contiguous(), c)
-                     for (i, f, c), w in zip(quads, widths)]
-            calls = [lambda t=t, l=None: c_call("hb_quad_fwd", t[0], t[1], t[2], 2, l) for t in quads]
-            kernel = "attn_fwd_kernel<4,128,1,false> (hb_quad_fwd)"
+            calls = [lambda t=t, l=None: abi_attention("hb_quad_fwd", q, k, v, out, l, *t, G, stream)
+                     for t in quad_tables(metas, T)]
         else:
             host = bridge_k_plan(tiles, kk, False, grid_size=grid)
-            tabs = [(ph.kv_indices.to(dev), ph.kv_counts.to(dev)) for ph in host.phases]
-            calls = [lambda t=t, l=None: c_call("hb_block_sparse_fwd", t[0], None, t[1], 0, l)
-                     for t in tabs]
-            kernel = "attn_fwd_kernel<1,128,1,false> (hb_block_sparse_fwd)"
+            calls = [lambda t=t, l=None: abi_attention("hb_block_sparse_fwd", q, k, v, out, l, t[0],
+                                                       None, t[1], G, stream)
+                     for t in [(ph.kv_indices.to(dev), ph.kv_counts.to(dev)) for ph in host.phases]]
+        kernel = KERNEL_NAMES[{"paired": "paired", "quad": "quad", "unpaired": "unpaired64"}[kind]]
         n_reps = reps if N < 32768 else max(3, reps // 2)
         med = []
         for fn in calls:
@@ -595,9 +604,12 @@ def main():
     ap.add_argument("--no-parity", action="store_true",
                     help="skip the in-run parity check (for kernel-trace runs, whose per-kernel "
                     "statistics it would crowd with its own fp32 reference kernels)")
-    ap.add_argument("--tables", choices=("paired", "paired128", "unpaired"), default="paired",
+    ap.add_argument("--tables", choices=("paired", "paired128", "unpaired", "quad", "unpaired64"),
+                    default="paired",
                     help="table format timed: paired 64-key blocks (the reference's default), paired "
-                    "128-key blocks, or the unpaired sparse_attention entry")
+                    "128-key blocks, the unpaired sparse_attention entry (paired on the device), quad "
+                    "256-query rows (hb_quad_fwd) or unpaired rows on the 64-query kernel "
+                    "(hb_block_sparse_fwd)")
     ap.add_argument("--full-tables", action="store_true",
                     help="time the kernel on all-connection tables instead (dense comparison for "
                     "counter runs: skipped blocks never touch HBM)")
@@ -685,7 +697,7 @@ def main():
     unpaired = None
     if a.tables == "paired128":
         metas = paired_plan_device(tiles, k, grid_size=grid, key_block_size=128, device=dev).phases
-    elif a.tables == "unpaired":
+    elif a.tables in ("unpaired", "unpaired64"):
         from hilberta_amd.bridge_k import bridge_k_plan
 
         host = bridge_k_plan(tiles, k, False, grid_size=grid)
@@ -711,14 +723,24 @@ def main():
     out = torch.empty_like(q)
 
     with torch.inference_mode():
-        if unpaired is None:
-            calls = [lambda m=m: paired_attention(q, k_, v, m, global_strategy="triton", num_warps=8,
-                                                  out=out) for m in metas]
+        # call(p, o, l): phase p's attention into o (and the LSE into l, when given)
+        if a.tables == "quad":
+            quads = quad_tables(metas, T)
+            call = lambda p, o, l=None: abi_attention("hb_quad_fwd", q, k_, v, o, l, *quads[p], G,  # noqa: E731
+                                                      stream)
+        elif a.tables == "unpaired64":
+            call = lambda p, o, l=None: abi_attention("hb_block_sparse_fwd", q, k_, v, o, l,  # noqa: E731
+                                                      unpaired[p][0], None, unpaired[p][1], G, stream)
+        elif unpaired is None:
+            call = lambda p, o, l=None: paired_attention(q, k_, v, metas[p], global_strategy="triton",  # noqa: E731
+                                                         num_warps=8, out=o, lse=l)
         else:
             from hilberta_amd.sparse_kernel import sparse_attention
 
-            calls = [lambda t=t: sparse_attention(q, k_, v, t[0], t[1], global_tokens=G,
-                                                  global_strategy="triton", out=out) for t in unpaired]
+            call = lambda p, o, l=None: sparse_attention(q, k_, v, unpaired[p][0], unpaired[p][1],  # noqa: E731
+                                                         global_tokens=G, global_strategy="triton",
+                                                         out=o, lse=l)
+        calls = [lambda p=p: call(p, out) for p in range(4)]
         for _ in range(a.warmup):
             for fn in calls:
                 fn()
@@ -839,14 +861,8 @@ def main():
         checks = []
         for p in range(0 if a.no_parity else 4):
             o = torch.empty_like(q)
-            if unpaired is None:
-                paired_attention(q, k_, v, metas[p], global_strategy="triton", num_warps=8, out=o,
-                                 lse=lse)
-                rows = row_lists(metas[p], N, G)
-            else:
-                sparse_attention(q, k_, v, unpaired[p][0], unpaired[p][1], global_tokens=G,
-                                 global_strategy="triton", out=o, lse=lse)
-                rows = row_lists(unpaired[p], N, G)
+            call(p, o, lse)
+            rows = row_lists(metas[p], N, G) if unpaired is None else row_lists(unpaired[p], N, G)
             checks.append(parity_check(o, lse, q, k_, v, rows, G, DIM ** -0.5))
             del o
         if checks:
