@@ -573,6 +573,67 @@ def config_figures(dev, stream, peak_measured, reps=10):
     return figs
 
 
+def ab_figures(dev, stream, other, rounds=7, reps=5):
+    """One-process A/B of the paired kernel against `other` ("quad" or "unpaired64") at every
+    BASELINE configuration: the same Q/K/V (seed 2707, drawn on the device) and the same layer
+    phases, both launch sequences interleaved round by round (the order alternating), each
+    round timing every phase `reps` times with HIP events; per configuration the phase-weighted
+    median ms of each kind and their ratio.  Outputs are compared after timing (max-abs of the
+    difference between the two kinds on phase 1)."""
+    from hilberta_amd.bridge_k import bridge_k_plan, paired_plan_device
+
+    cases = [("1024_t4k1", 1), ("1024_t4k1", 4), ("1024_t16k3", 1), ("2048_t4k1", 1),
+             ("2048_t16k3", 1), ("4096_t16k3", 1)]
+    figs = {}
+    for name, batch in cases:
+        grid, tiles, kk = CONFIGS[name]
+        plan = paired_plan_device(tiles, kk, grid_size=grid, device=dev)
+        N, G = plan.total_tokens, plan.global_tokens
+        T = N // 64
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(2707)
+        q, k, v = (torch.randn(batch, HEADS, N, DIM, device=dev, generator=gen).to(torch.bfloat16)
+                   for _ in range(3))
+        outs = {"paired": torch.empty_like(q), other: torch.empty_like(q)}
+        metas = plan.phases
+        calls = {"paired": [lambda m=m: abi_attention("hb_paired_fwd", q, k, v, outs["paired"], None,
+                                                      m.kv_indices, m.kv_flags, m.kv_counts, G, stream)
+                            for m in metas]}
+        if other == "quad":
+            calls[other] = [lambda t=t: abi_attention("hb_quad_fwd", q, k, v, outs[other], None, *t,
+                                                      G, stream) for t in quad_tables(metas, T)]
+        else:
+            host = bridge_k_plan(tiles, kk, False, grid_size=grid)
+            tabs = [(ph.kv_indices.to(dev), ph.kv_counts.to(dev)) for ph in host.phases]
+            calls[other] = [lambda t=t: abi_attention("hb_block_sparse_fwd", q, k, v, outs[other],
+                                                      None, t[0], None, t[1], G, stream)
+                            for t in tabs]
+        times = {kind: [[] for _ in metas] for kind in calls}
+        for kind in calls:
+            for fn in calls[kind]:
+                fn()
+        for r in range(rounds):
+            order = ("paired", other) if r % 2 == 0 else (other, "paired")
+            for kind in order:
+                for p, fn in enumerate(calls[kind]):
+                    times[kind][p] += event_time(fn, reps, stream)
+        ms = {}
+        for kind in calls:
+            med = [statistics.median(t) for t in times[kind]]
+            ms[kind] = sum(w * t for w, t in zip(WEIGHTS, med)) / sum(WEIGHTS)
+        calls["paired"][1]()
+        calls[other][1]()
+        torch.cuda.synchronize()
+        diff = (outs["paired"].float() - outs[other].float()).abs().max().item()
+        label = f"{name}_b{batch}"
+        figs[label] = {"paired_ms": round(ms["paired"], 4), f"{other}_ms": round(ms[other], 4),
+                       "ratio": round(ms[other] / ms["paired"], 4), "max_abs_diff_phase1": diff}
+        log(f"  A/B {label}: paired {ms['paired']:.4f} ms, {other} {ms[other]:.4f} ms "
+            f"({ms[other] / ms['paired']:.3f}x), max|diff| {diff:.2e}")
+        del q, k, v, outs
+    return figs
+
+
 def cpu_table_build_ms(tiles, k, grid):
     """The oracle's numpy table build (bridge_k_plan + pair_metadata, four phases) on the host."""
     root = os.path.dirname(os.path.abspath(__file__))
@@ -625,6 +686,9 @@ def main():
     ap.add_argument("--layout-probe", action="store_true",
                     help="only run the permutation gathers ([B, n, 3072] and [B, n, 64] bf16) and "
                     "the device table build of --config, 5 times each (for counter runs)")
+    ap.add_argument("--ab", choices=("quad", "unpaired64"), default=None,
+                    help="only run a one-process A/B of the paired kernel against quad or unpaired "
+                    "64-query tables at every configuration (interleaved rounds), one JSON line")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py runs on one GPU: --gpus {a.gpus} is not supported in this build "
@@ -645,6 +709,14 @@ def main():
 
     if a.denoiser:
         denoiser_bench(a)
+        return
+
+    if a.ab:
+        dev = torch.device("cuda:0")
+        torch.cuda.set_device(dev)
+        figs = ab_figures(dev, torch.cuda.current_stream(dev), a.ab)
+        print(json.dumps({"ab": f"paired vs {a.ab}", "unit": "ms per call (phase-weighted)",
+                          "configs": figs}), flush=True)
         return
 
     if a.layout_probe:
