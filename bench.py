@@ -56,7 +56,10 @@ KERNEL_NAMES = {"paired": "attn_fwd_kernel<2,128,1,false> (hb_paired_fwd)",
                 # pairable 64-query tables: pair_rows_kernel (hb_pair_rows) + the paired kernel
                 "unpaired": "attn_fwd_kernel<2,128,1,false> (hb_pair_rows + hb_paired_fwd)",
                 "quad": "attn_fwd_kernel<4,128,1,false> (hb_quad_fwd)",
-                "unpaired64": "attn_fwd_kernel<1,128,1,false> (hb_block_sparse_fwd)"}
+                "unpaired64": "attn_fwd_kernel<1,128,1,false> (hb_block_sparse_fwd)",
+                # tables that pair only with an overhanging half (odd row count, G an odd
+                # multiple of 64): sparse_attention pairs them from the end
+                "ragged": "attn_fwd_kernel<2,128,1,false> (hb_pair_rows + hb_paired_fwd)"}
 TABLE_NAMES = {"paired": "paired", "paired128": "paired KV128", "unpaired": "unpaired (sparse_attention)",
                "quad": "quad (256-query rows)", "unpaired64": "unpaired, 64-query kernel"}
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
@@ -514,13 +517,16 @@ def config_figures(dev, stream, peak_measured, reps=10):
     configuration the phase-weighted ms of paired_attention, live TFLOP/s, the fraction of the
     nominal and of the measured MFMA peak, and a sampled parity check.  Q/K/V are drawn on the
     device from seed 2707 (as benchmark.py:24-28 does).  Also the same 2048 px 16-tile K3 call on
-    the quad (256-query) kernel and on the unpaired 64-query kernel, through the C ABI."""
+    the quad (256-query) kernel and on the unpaired 64-query kernel, through the C ABI; and a
+    ragged shape (the first ordinary 64-query row promoted to the global prefix, G = 576 and 255
+    rows, neither pairing evenly) through sparse_attention, which pairs it from the end with an
+    overhanging half, against the same tables on the unpaired 64-query kernel."""
     from hilberta_amd.bridge_k import bridge_k_plan, paired_plan_device
     from hilberta_amd.paired_kernel import paired_attention
 
     cases = [("1024_t4k1", 1, "paired"), ("1024_t4k1", 4, "paired"), ("1024_t16k3", 1, "paired"),
              ("2048_t4k1", 1, "paired"), ("4096_t16k3", 1, "paired"), ("2048_t16k3", 1, "quad"),
-             ("2048_t16k3", 1, "unpaired")]
+             ("2048_t16k3", 1, "unpaired"), ("2048_t16k3", 1, "ragged"), ("2048_t16k3", 1, "ragged64")]
     figs = {}
     for name, batch, kind in cases:
         grid, tiles, kk = CONFIGS[name]
@@ -541,25 +547,42 @@ def config_figures(dev, stream, peak_measured, reps=10):
         elif kind == "quad":
             calls = [lambda t=t, l=None: abi_attention("hb_quad_fwd", q, k, v, out, l, *t, G, stream)
                      for t in quad_tables(metas, T)]
-        else:
+        elif kind == "unpaired":
             host = bridge_k_plan(tiles, kk, False, grid_size=grid)
             calls = [lambda t=t, l=None: abi_attention("hb_block_sparse_fwd", q, k, v, out, l, t[0],
                                                        None, t[1], G, stream)
                      for t in [(ph.kv_indices.to(dev), ph.kv_counts.to(dev)) for ph in host.phases]]
-        kernel = KERNEL_NAMES[{"paired": "paired", "quad": "quad", "unpaired": "unpaired64"}[kind]]
+        else:
+            from hilberta_amd.sparse_kernel import sparse_attention
+
+            # first ordinary row promoted to the prefix: its queries see every key
+            host = bridge_k_plan(tiles, kk, False, grid_size=grid)
+            G = G + 64
+            tabs = [(ph.kv_indices[1:].contiguous().to(dev), ph.kv_counts[1:].contiguous().to(dev))
+                    for ph in host.phases]
+            live = [(G // 64) * T + int(c.sum()) for _, c in tabs]
+            if kind == "ragged":
+                calls = [lambda t=t, l=None: sparse_attention(q, k, v, t[0], t[1], global_tokens=G,
+                                                              out=out, lse=l) for t in tabs]
+            else:
+                calls = [lambda t=t, l=None: abi_attention("hb_block_sparse_fwd", q, k, v, out, l,
+                                                           t[0], None, t[1], G, stream) for t in tabs]
+        kernel = KERNEL_NAMES[{"paired": "paired", "quad": "quad", "unpaired": "unpaired64",
+                               "ragged": "ragged", "ragged64": "unpaired64"}[kind]]
         n_reps = reps if N < 32768 else max(3, reps // 2)
-        med = []
-        for fn in calls:
-            for _ in range(2):
+        # every phase warmed before any is timed (the first phase timed otherwise reads 5-15 %
+        # slow while the clock ramps)
+        for _ in range(2):
+            for fn in calls:
                 fn()
-            med.append(statistics.median(event_time(fn, n_reps, stream)))
+        med = [statistics.median(event_time(fn, n_reps, stream)) for fn in calls]
         weighted = sum(w * t for w, t in zip(WEIGHTS, med)) / sum(WEIGHTS)
         flops = [4 * DIM * 64 * 64 * HEADS * batch * lb for lb in live]
         w_flops = sum(w * f for w, f in zip(WEIGHTS, flops)) / sum(WEIGHTS)
         tf = w_flops / (weighted * 1e-3) / 1e12
         # sampled parity on phase 1 (every kind writes out / lse of the same call)
         calls[1](l=lse)
-        rows = row_lists(metas[1], N, G)
+        rows = row_lists(tabs[1] if kind.startswith("ragged") else metas[1], N, G)
         picks = sorted({0, len(rows) - 1, *range(0, len(rows), max(1, len(rows) // 6))})
         par = sampled_parity(out, lse, q, k, v, rows, G, DIM ** -0.5, picks)
         label = f"{name}_b{batch}" + ("" if kind == "paired" else f"_{kind}")

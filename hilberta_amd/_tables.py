@@ -201,7 +201,8 @@ def pair_rows_device(kv_indices, kv_counts, total_blocks, *, key_block_size=64, 
     """Pair an unpaired device table in one launch, without a host synchronisation.
 
     The device form of ``pair_metadata`` (reference hilberta/paired_metadata.py:26-51): rows 2r
-    and 2r + 1 become paired row r, ascending, flag bit (half + 2*key_half), zero-padded to
+    and 2r + 1 become paired row r (an odd row count is paired from the end: rows 2r - 1 and 2r,
+    paired row 0 with an empty half 0), ascending, flag bit (half + 2*key_half), zero-padded to
     ``paired_width``, which should bound every paired row's entry count (min(2 * width, key
     blocks) always does).  ``overflow`` may be a device int32 scalar tensor that is set to 1 when
     some paired row had to be cut to ``paired_width`` entries.  Returns (ids, flags, counts) as
@@ -209,9 +210,10 @@ def pair_rows_device(kv_indices, kv_counts, total_blocks, *, key_block_size=64, 
     """
     device = kv_indices.device
     rows, width = kv_indices.shape
-    ids = torch.empty((rows // 2, paired_width), dtype=torch.int32, device=device)
+    prows = (rows + 1) // 2
+    ids = torch.empty((prows, paired_width), dtype=torch.int32, device=device)
     flags = torch.empty_like(ids)
-    counts = torch.empty((rows // 2,), dtype=torch.int32, device=device)
+    counts = torch.empty((prows,), dtype=torch.int32, device=device)
     rc = _lib.load().hb_pair_rows(kv_indices.data_ptr(), kv_counts.data_ptr(), rows, width,
                                   total_blocks, key_block_size, ids.data_ptr(), flags.data_ptr(),
                                   counts.data_ptr(), paired_width,

@@ -74,7 +74,7 @@ struct AttnArgs {
   const int32_t* indices;
   const int32_t* flags;
   const int32_t* counts;
-  int32_t heads, tokens, bh, width, rows, key_blocks;
+  int32_t heads, tokens, global_tokens, bh, width, rows, key_blocks;
   int32_t global_tiles, nsplit, chunk, per_bh;
   float scale_log2;
   int32_t* counters;  // [0, 8) queue heads, [8] exit count, [9] drained-queue mask; zero between launches
@@ -388,8 +388,12 @@ __global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, 
   auto load_q = [&](const Item& it) {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
+      // (a paired row's first item may start 64 queries before token 0 when G = 0 and the
+      // ordinary query count is an odd multiple of 64: that half is never stored, and loads the
+      // queries of token 0 instead)
+      const int qi = max(it.qfirst + wave * QW + g * 32 + ql, 0);
       const uint16_t* qp = a.q + (int64_t)it.b * a.q_sb + (int64_t)it.h * a.q_sh +
-                           (int64_t)(it.qfirst + wave * QW + g * 32 + ql) * a.q_sn + hl * 8;
+                           (int64_t)qi * a.q_sn + hl * 8;
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) qreg[g][ds] = *(const u32x4*)(qp + ds * 16);
     }
@@ -519,8 +523,11 @@ __global__ __launch_bounds__(128 * HALVES, (HALVES == 2 ? groups_per_cu<HALVES, 
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       const float l_tot = pair_sum(l_run[g]);
-      const int q = cur.qfirst + wave * QW + g * 32 + ql;
       if (!cur.global || a.nsplit == 1) {
+        // 32 queries outside the item's own range (the half of a paired row that reaches into the
+        // global prefix, or of the last global tile past it) are computed but not stored
+        const int q0 = cur.qfirst + wave * QW + g * 32;
+        if (cur.global ? q0 >= a.global_tokens : q0 < a.global_tokens) continue;
         const float inv = 1.f / l_tot;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
@@ -784,6 +791,9 @@ __global__ __launch_bounds__(128 * HALVES) void merge_kernel(AttnArgs a) {
   const int bh = tile / a.global_tiles, gtile = tile - bh * a.global_tiles;
   const int b = bh / a.heads, h = bh - b * a.heads;
   const int64_t sl0 = (int64_t)tile * a.nsplit * WAVES + wave;
+  // the 64 queries of a last global tile that reach past the global prefix (G an odd multiple of
+  // 64, paired tables) belong to the first ordinary row, whose item stores them
+  if (gtile * QT + wave * 32 >= a.global_tokens) return;
   const int q = gtile * QT + wave * 32 + ql;
   uint16_t* op = a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)q * a.o_sn + hl * 4 + dt * 32;
   if (a.nsplit <= 4) {
@@ -880,12 +890,16 @@ int make_plan(Plan& p, int batch, int heads, int tokens, int head_dim, int globa
   HB_REQUIRE(key_block_size == 64 || (paired && key_block_size == 128),
              "key_block_size must be 64 (or 128 with paired tables)");
   p.kbr = key_block_size / 64;
-  HB_REQUIRE(tokens % p.qt == 0 && global_tokens % p.qt == 0 && global_tokens >= 0 &&
+  // Paired tables take N and G in multiples of 64: rows are aligned to the end of the sequence
+  // (the first one may reach 64 queries into the global prefix) and global tiles to its start
+  // (the last one may reach 64 queries past G); the kernel stores neither overhang.
+  const int align = p.halves == 2 ? 64 : p.qt;
+  HB_REQUIRE(tokens % align == 0 && global_tokens % align == 0 && global_tokens >= 0 &&
                  global_tokens < tokens,
-             "tokens and global_tokens must be multiples of %d with ordinary queries remaining", p.qt);
-  p.rows = (tokens - global_tokens) / p.qt;
+             "tokens and global_tokens must be multiples of %d with ordinary queries remaining", align);
+  p.rows = (tokens - global_tokens + p.qt - 1) / p.qt;
   p.key_blocks = tokens / 64;
-  p.global_tiles = all_queries ? global_tokens / p.qt : 0;
+  p.global_tiles = all_queries ? (global_tokens + p.qt - 1) / p.qt : 0;
   // A global query tile sweeps every key block.  It is split into at most MAX_SPLIT chunks of
   // about half the average work of one workgroup (at the nominal 2 workgroups x 256 CUs), and
   // never shorter than the longest ordinary row or than MIN_CHUNK steps: the chunks are claimed
@@ -989,6 +1003,7 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, float*
   a.counts = kv_counts;
   a.heads = heads;
   a.tokens = tokens;
+  a.global_tokens = global_tokens;
   a.bh = batch * heads;
   a.width = table_width;
   a.rows = p.rows;

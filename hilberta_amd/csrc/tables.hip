@@ -503,16 +503,18 @@ extern "C" int hb_bits_emit(const uint32_t* bits, int32_t rows, int32_t total_bl
 }
 
 // Pairs an unpaired table in one launch (pair_metadata, paired_metadata.py:26-51): one wave per
-// paired row r builds the key-block bitmaps of rows 2r and 2r + 1 in LDS, then writes their union
-// in ascending key-block order with flag bit (half + 2*key_half) set where row `half` holds key
-// half `key_half`, zero-pads the row to out_width and stores its count.  Ids outside [0, T) and
-// entries past a row's count (clamped to width) are ignored.  A union longer than out_width is
-// cut to out_width entries and sets *overflow (when given) to 1.
+// paired row r builds the key-block bitmaps of rows 2r - lead and 2r + 1 - lead in LDS, then writes
+// their union in ascending key-block order with flag bit (half + 2*key_half) set where row `half`
+// holds key half `key_half`, zero-pads the row to out_width and stores its count.  lead is 1 for
+// an odd row count: paired rows are aligned to the end of the table (as the attention kernel
+// aligns them to the end of the sequence), so paired row 0 holds an empty half 0 and row 0 as
+// half 1.  Ids outside [0, T) and entries past a row's count (clamped to width) are ignored.  A
+// union longer than out_width is cut to out_width entries and sets *overflow (when given) to 1.
 constexpr int PAIR_MAX_BLOCKS = 2048;  // key blocks per row the LDS bitmaps cover
 constexpr int PAIR_WORDS = PAIR_MAX_BLOCKS / 32 + 2;
 __global__ __launch_bounds__(TPB) void pair_rows_kernel(const int32_t* ids, const int32_t* counts,
-                                                        int prows, int width, int T, int ratio,
-                                                        int out_width, int32_t* out_ids,
+                                                        int prows, int lead, int width, int T,
+                                                        int ratio, int out_width, int32_t* out_ids,
                                                         int32_t* out_flags, int32_t* out_counts,
                                                         int32_t* overflow) {
   __shared__ uint32_t bm[TPB / 64][2][PAIR_WORDS];
@@ -522,7 +524,8 @@ __global__ __launch_bounds__(TPB) void pair_rows_kernel(const int32_t* ids, cons
   __syncthreads();
   if (pr < prows) {
     for (int h = 0; h < 2; ++h) {
-      const int row = 2 * pr + h;
+      const int row = 2 * pr + h - lead;
+      if (row < 0) continue;  // the empty half of an odd table's first paired row
       const int c = min(max(counts[row], 0), width);
       const int32_t* rid = ids + (int64_t)row * width;
       for (int e = lane; e < c; e += 64) {
@@ -564,15 +567,16 @@ extern "C" int hb_pair_rows(const int32_t* kv_indices, const int32_t* kv_counts,
                             int32_t paired_width, int32_t* overflow, hb_stream_t stream) {
   HB_REQUIRE(kv_indices && kv_counts && paired_ids && paired_flags && paired_counts,
              "null pointer argument");
-  HB_REQUIRE(rows > 0 && rows % 2 == 0, "rows must be positive and even (got %d)", rows);
+  HB_REQUIRE(rows > 0, "rows must be positive (got %d)", rows);
   HB_REQUIRE(width > 0 && paired_width > 0, "table widths must be positive");
   HB_REQUIRE(total_blocks > 0 && total_blocks <= PAIR_MAX_BLOCKS,
              "total_blocks must be in [1, %d] (got %d)", PAIR_MAX_BLOCKS, total_blocks);
   HB_REQUIRE(key_block_size == 64 || key_block_size == 128, "key_block_size must be 64 or 128");
-  const int prows = rows / 2, per_block = TPB / 64;
+  const int lead = rows & 1, prows = (rows + 1) / 2, per_block = TPB / 64;
   hipLaunchKernelGGL(pair_rows_kernel, dim3((prows + per_block - 1) / per_block), dim3(TPB), 0,
-                     stream, kv_indices, kv_counts, prows, width, total_blocks, key_block_size / 64,
-                     paired_width, paired_ids, paired_flags, paired_counts, overflow);
+                     stream, kv_indices, kv_counts, prows, lead, width, total_blocks,
+                     key_block_size / 64, paired_width, paired_ids, paired_flags, paired_counts,
+                     overflow);
   HB_HIP(hipGetLastError());
   return HB_OK;
 }

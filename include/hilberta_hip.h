@@ -49,7 +49,13 @@ int64_t hb_attention_workspace_bytes(int32_t batch, int32_t heads, int32_t token
  *   q, k, v, out : [B, H, N, D] bf16/fp16 views, last dim contiguous, 16-byte aligned base
  *   lse          : optional fp32 [B, H, N] natural-log row logsumexp (NULL to skip)
  *   strides      : 12 element strides: q(b,h,n), k(b,h,n), v(b,h,n), out(b,h,n)
- *   kv_indices, kv_flags : int32 [(N-G)/128, table_width]; kv_counts int32 [(N-G)/128]
+ *   kv_indices, kv_flags : int32 [ceil((N-G)/128), table_width]; kv_counts int32 [ceil((N-G)/128)]
+ *   N and G     : multiples of 64.  Paired rows are aligned to the end of the sequence: row r
+ *                  covers queries N - 128*(rows - r) ..+127, so when N - G is an odd multiple of 64
+ *                  row 0's half 0 lies in the global prefix; it is computed but never stored (its
+ *                  flags should be 0; hb_pair_rows leaves it empty).  When G is an odd multiple of
+ *                  64 the last 128-query global tile reaches 64 queries past G; they are computed
+ *                  but never stored either.  (The reference requires N and G multiples of 128.)
  *   key_block_size : 64 or 128 (flag bit half + 2*key_half)
  *   all_queries  : 1 = global query rows attend every key block in this launch
  *                  (the reference's "triton" strategy); 0 = leave global rows untouched
@@ -210,8 +216,11 @@ int hb_bits_emit(const uint32_t* bits, int32_t rows, int32_t total_blocks, int32
 
 /* Pairs an unpaired table in one launch, replacing pair_metadata (paired_metadata.py:26-51) on the
  * device: rows 2r and 2r + 1 of kv_indices [rows, width] (with kv_counts) become paired row r of
- * paired_ids / paired_flags [rows/2, paired_width], ascending, flag bit (half + 2*key_half),
- * zero-padded, and paired_counts [rows/2].  paired_width should bound every paired row's entries
+ * paired_ids / paired_flags [(rows+1)/2, paired_width], ascending, flag bit (half + 2*key_half),
+ * zero-padded, and paired_counts [(rows+1)/2].  An odd row count is paired from the end: paired
+ * row r then holds rows 2r - 1 and 2r, and paired row 0 has an empty half 0 (the layout
+ * hb_paired_fwd expects for ordinary query counts that are odd multiples of 64; pair_metadata
+ * itself rejects odd counts).  paired_width should bound every paired row's entries
  * (min(2*width, key blocks) always does): a longer row is cut to paired_width entries and sets
  * *overflow (device int32, may be NULL; never cleared here) to 1.  total_blocks <= 2048.  No host
  * synchronisation. */

@@ -99,8 +99,8 @@ def test_global_tile_split_plan():
 def test_pair_rows_rejections():
     lib = _lib.load()
     buf = ctypes.c_void_p(16)  # never dereferenced: every call below fails its argument checks
-    rc = lib.hb_pair_rows(buf, buf, 3, 4, 72, 64, buf, buf, buf, 8, None, None)
-    assert rc == 1 and "even" in _lib.last_error()
+    rc = lib.hb_pair_rows(buf, buf, 0, 4, 72, 64, buf, buf, buf, 8, None, None)
+    assert rc == 1 and "rows must be positive" in _lib.last_error()
     rc = lib.hb_pair_rows(buf, buf, 4, 4, 4096, 64, buf, buf, buf, 8, None, None)
     assert rc == 1 and "total_blocks" in _lib.last_error()
     rc = lib.hb_pair_rows(buf, buf, 4, 4, 72, 96, buf, buf, buf, 8, None, None)

@@ -153,32 +153,55 @@ def test_unpaired_tables_run_paired(hip_device):
         assert (lse[:, :, :G] - ref_l[:, :, :G]).abs().max().item() <= 1e-3
 
 
-def test_unpaired_odd_rows_use_unpaired_kernel(hip_device):
-    """Tables whose 64-query rows do not pair (an odd number of them) run on the 64-query-row
-    kernel; against the fp32 oracle on random valid tables."""
-    from hilberta_amd.sparse_kernel import sparse_attention
-
-    G, rows = 512, 9
-    N = G + 64 * rows
-    T_ = N // 64
-    rng = np.random.default_rng(5)
-    width = G // 64 + 6
+def _random_rows(G, rows, seed, max_extra=7):
+    """Random valid unpaired tables: every row holds the global prefix plus 1..max_extra-1 other
+    key blocks, ascending."""
+    T_ = G // 64 + rows
+    rng = np.random.default_rng(seed)
+    width = G // 64 + max_extra
     ids = np.zeros((rows, width), np.int32)
     counts = np.zeros(rows, np.int32)
     for r in range(rows):
-        extra = rng.choice(np.arange(G // 64, T_), size=rng.integers(1, 7), replace=False)
+        size = rng.integers(1, min(max_extra, T_ - G // 64 + 1))
+        extra = rng.choice(np.arange(G // 64, T_), size=size, replace=False)
         row = np.concatenate([np.arange(G // 64), np.sort(extra)]).astype(np.int32)
         ids[r, :len(row)] = row
         counts[r] = len(row)
-    q, k, v = A.seeded_qkv(1, 3, N, D, seed=8)
+    return ids, counts
+
+
+@pytest.mark.parametrize("G,rows,dim", [
+    (512, 9, 128),   # odd row count: paired row 0 reaches 64 queries into the global prefix
+    (576, 8, 128),   # G an odd multiple of 64: the last global tile reaches 64 queries past G
+    (576, 9, 64),    # both
+    (0, 7, 128),     # no prefix and an odd row count: the empty half lies before token 0
+    (64, 5, 128),    # one global 64-query row
+    (576, 71, 128),  # 80 key blocks: the global tiles split, merge_kernel skips the overhang
+])
+def test_ragged_tables_run_paired(hip_device, G, rows, dim):
+    """Tables whose 64-query rows do not pair evenly (an odd row count, or a global prefix that is
+    an odd multiple of 64) are paired from the end on the device and run on the paired kernel:
+    every row against the fp32 oracle, and the ordinary rows bit for bit equal to the unpaired
+    64-query-row kernel's (same blocks, same order, same arithmetic)."""
+    from hilberta_amd.sparse_kernel import sparse_attention
+
+    N = G + 64 * rows
+    ids, counts = _random_rows(G, rows, seed=5 + rows + G)
+    q, k, v = A.seeded_qkv(1, 3, N, dim, seed=8)
     qd, kd, vd = (x.to(hip_device) for x in (q, k, v))
-    say(f"case unpaired odd rows N={N}")
-    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=hip_device)
-    out = sparse_attention(qd, kd, vd, torch.from_numpy(ids).to(hip_device),
-                           torch.from_numpy(counts).to(hip_device), global_tokens=G, lse=lse)
+    say(f"case ragged tables G={G} rows={rows} D={dim} N={N}")
+    idd, cnd = torch.from_numpy(ids).to(hip_device), torch.from_numpy(counts).to(hip_device)
+    lse = torch.full(q.shape[:3], float("nan"), dtype=torch.float32, device=hip_device)
+    out = torch.full_like(qd, float("nan"))
+    sparse_attention(qd, kd, vd, idd, cnd, global_tokens=G, lse=lse, out=out)
     torch.cuda.synchronize()
     ref_o, ref_l = A.block_sparse_attention(q, k, v, ids, counts, global_tokens=G)
-    compare(out.cpu(), lse.cpu(), ref_o, ref_l, "unpaired odd rows")
+    compare(out.cpu(), lse.cpu(), ref_o, ref_l, f"ragged G={G} rows={rows}")
+    if dim == 128:
+        uo, ul = _unpaired_kernel(qd, kd, vd, idd, cnd, G, dim ** -0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(out[:, :, G:], uo[:, :, G:]), "ordinary rows differ from the unpaired kernel"
+        assert torch.equal(lse[:, :, G:], ul[:, :, G:]), "ordinary LSE differs from the unpaired kernel"
 
 
 @pytest.mark.parametrize("dtype,dim", [(torch.float16, 128), (torch.bfloat16, 64), (torch.float16, 64)])

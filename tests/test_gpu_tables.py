@@ -258,6 +258,44 @@ def test_pair_rows_equals_pair_metadata(hip_device, name, phase, kb):
     assert not ids[:, rw:].any() and not flags[:, rw:].any()
 
 
+@pytest.mark.parametrize("kb", [64, 128])
+def test_pair_rows_odd_row_count(hip_device, kb):
+    """An odd row count is paired from the end.  Rows 1..63 of a 64-row table: paired row 0 holds
+    row 1 alone as half 1 (an empty half 0, so flag bits 2 + 8 * key_half only), and paired rows
+    r > 0 hold rows 2r and 2r + 1 of the full table, bit-exact with pair_metadata's rows r > 0."""
+    from hilberta_amd._tables import pair_rows_device
+
+    plan = oracle_plan("1024_t16k3")
+    p = plan["phases"][2]
+    full = oracle_paired(plan, 2, key_block_size=kb)
+    ids_np = np.ascontiguousarray(np.asarray(p["kv_indices"])[1:])
+    counts_np = np.ascontiguousarray(np.asarray(p["kv_counts"])[1:])
+    rows, width = ids_np.shape
+    blocks = plan["total_tokens"] // 64
+    pwidth = min(2 * width, -(-blocks // (kb // 64)))
+    say(f"case pair_rows odd rows={rows} KB{kb}")
+    pid, pfl, pct = pair_rows_device(torch.from_numpy(ids_np).to(hip_device),
+                                     torch.from_numpy(counts_np).to(hip_device), blocks,
+                                     key_block_size=kb, paired_width=pwidth)
+    torch.cuda.synchronize()
+    pid, pfl, pct = pid.cpu().numpy(), pfl.cpu().numpy(), pct.cpu().numpy()
+    assert pid.shape == ((rows + 1) // 2, pwidth)
+    # paired row 0: the first remaining row alone, as half 1
+    r = kb // 64
+    exp0 = {}
+    for b in ids_np[0, :counts_np[0]].tolist():
+        exp0[b // r] = exp0.get(b // r, 0) | (1 << (1 + 2 * (b % r)))
+    keys = sorted(exp0)
+    assert pct[0] == len(keys)
+    assert pid[0, :pct[0]].tolist() == keys and pfl[0, :pct[0]].tolist() == [exp0[b] for b in keys]
+    assert not pid[0, pct[0]:].any() and not pfl[0, pct[0]:].any()
+    ref_ids, ref_flags, ref_counts = (np.asarray(full[k])[1:] for k in ("kv_indices", "kv_flags", "kv_counts"))
+    rw = ref_ids.shape[1]
+    assert np.array_equal(pct[1:], ref_counts)
+    assert np.array_equal(pid[1:, :rw], ref_ids) and np.array_equal(pfl[1:, :rw], ref_flags)
+    assert not pid[1:, rw:].any() and not pfl[1:, rw:].any()
+
+
 def test_pair_rows_reports_overflow(hip_device):
     """A paired width below the widest union cuts those rows to the width and raises the
     overflow word; the exact width (the widest union of pair_metadata) leaves it at zero."""
