@@ -127,3 +127,26 @@ def test_noalloc_rejects_shapes_beyond_its_scratch():
     rc = lib.hb_paired_fwd_noalloc(buf, buf, buf, buf, None, strides, 1, 24, 16896, 96, 0, buf, buf,
                                    buf, 24, 512, 64, 1, 1.0, 0, None)
     assert rc == 1 and "head_dim" in _lib.last_error()
+
+
+def test_paired_ragged_shapes():
+    """Paired launches take N and G in multiples of 64: ceil((N-G)/128) rows aligned to the end
+    of the sequence and ceil(G/128) global tiles, the last of which overhangs G when G is an odd
+    multiple of 64; the split partials in the workspace count that tile whole."""
+    lib = _lib.load()
+    per_chunk = 4 * (4 * 16 * 64 * 4 + 128 * 4)  # four waves' fragments and (max, sum) rows
+    for G, tiles in ((512, 4), (576, 5), (64, 1)):
+        N = 16896 + (G - 512)
+        ws = lib.hb_attention_workspace_bytes(1, 24, N, 128, G, 28, 64, 1, 1)
+        assert (ws - 256) == 24 * tiles * 3 * per_chunk, (G, ws)  # three chunks of 88 blocks
+    assert lib.hb_attention_workspace_bytes(1, 24, 16384, 128, 0, 28, 64, 1, 1) == 256
+    # N - G an odd multiple of 64 is accepted; N or G off the 64 grid is not
+    assert lib.hb_attention_workspace_bytes(1, 24, 16896 - 64, 128, 512, 28, 64, 1, 1) > 256
+    assert lib.hb_attention_workspace_bytes(1, 24, 16896 - 32, 128, 512, 28, 64, 1, 1) == -1
+    assert lib.hb_attention_workspace_bytes(1, 24, 16896, 128, 544, 28, 64, 1, 1) == -1
+    # quad tables keep multiples of 256
+    assert lib.hb_attention_workspace_bytes(1, 24, 16896 - 128, 128, 512, 28, 64, 2, 1) == -1
+    # hb_pair_rows takes odd row counts (paired from the end); only the count's sign is checked
+    buf = ctypes.c_void_p(16)
+    rc = lib.hb_pair_rows(buf, buf, -3, 4, 72, 64, buf, buf, buf, 8, None, None)
+    assert rc == 1 and "rows must be positive" in _lib.last_error()
