@@ -857,6 +857,8 @@ def main():
             per_phase[p].append(s.elapsed_time(e))
         med = [statistics.median(x) for x in per_phase]
         weighted = sum(w * t for w, t in zip(WEIGHTS, med)) / sum(WEIGHTS)
+        means = [statistics.fmean(x) for x in per_phase]
+        weighted_mean = sum(w * t for w, t in zip(WEIGHTS, means)) / sum(WEIGHTS)
         flops = [4 * DIM * 64 * 64 * HEADS * a.batch * lb for lb in live]
         tflops = [f / (t * 1e-3) / 1e12 for f, t in zip(flops, med)]
         w_flops = sum(w * f for w, f in zip(WEIGHTS, flops)) / sum(WEIGHTS)
@@ -1002,6 +1004,9 @@ def main():
             "parallelism": "single GPU",
         },
         "phase_ms": [round(x, 4) for x in med],
+        # the mean over the timed calls, for comparison with a profiler's average per dispatch
+        "phase_mean_ms": [round(x, 4) for x in means],
+        "call_mean_ms": round(weighted_mean, 4),
         "phase_p10_ms": [round(q10(x, 0.1), 4) for x in per_phase],
         "phase_p90_ms": [round(q10(x, 0.9), 4) for x in per_phase],
         "live_blocks": live,
