@@ -5,9 +5,9 @@
 //
 //  * Work item = one query tile (256 queries for quad tables, 128 for paired tables, 64 for
 //    unpaired ones) of one (batch, head), or one chunk of a global (text) query tile's all-key
-//    sweep.  Global tiles are
-//    split into at most MAX_SPLIT chunks of about half a workgroup's average work, none shorter
-//    than the longest ordinary row or MIN_CHUNK steps, so no item dominates the schedule; chunk
+//    sweep.  Global tiles are split into at most MAX_SPLIT chunks of about a workgroup's average
+//    work (at least two for sweeps of four rows or more), none shorter than the longest ordinary
+//    row or MIN_CHUNK steps, so no item dominates the schedule; chunk
 //    partials (unnormalised accumulator, running max, row sum) go to the workspace and
 //    merge_kernel combines them after the main kernel.
 //  * Persistent workgroups (2 per CU; 3 for paired D = 64 calls with enough items; 1 eight-wave
@@ -901,21 +901,24 @@ int make_plan(Plan& p, int batch, int heads, int tokens, int head_dim, int globa
   p.key_blocks = tokens / 64;
   p.global_tiles = all_queries ? (global_tokens + p.qt - 1) / p.qt : 0;
   // A global query tile sweeps every key block.  It is split into at most MAX_SPLIT chunks of
-  // about half the average work of one workgroup (at the nominal 2 workgroups x 256 CUs), and
-  // never shorter than the longest ordinary row or than MIN_CHUNK steps: the chunks are claimed
-  // first, so each finishes well before the queues drain, while few chunks keep the partials and
-  // the merge small.  The average is estimated from the table width, which overstates the row
-  // work by up to 2x for tables padded to a bound (rows paired on the device); half of it keeps
-  // the chunks short enough there and costs nothing on tables of exact width.
+  // about the average work of one workgroup (at the nominal 2 workgroups x 256 CUs), never
+  // shorter than the longest ordinary row or than MIN_CHUNK steps, and into at least two when the
+  // sweep is four rows long or more: the chunks are claimed first, so each finishes well before
+  // the queues drain, while few chunks keep the partials and the merge small.  The average is
+  // estimated from the table width, which overstates the row work by up to 2x for tables padded
+  // to a bound (rows paired on the device); the two-chunk floor keeps a whole sweep from ending
+  // in the tail there.  (Against half the average: 2048 px 0.7-0.9 % faster with two chunks
+  // instead of three, or none at 4-tile K1; the padded tables and the other shapes unchanged.)
   const int64_t row_steps = (int64_t)width * p.kbr;
   const int64_t all_steps =
       (int64_t)batch * heads * ((int64_t)p.rows * row_steps + (int64_t)p.global_tiles * p.key_blocks);
   // (quad workgroups are half as many, one per CU)
   const int64_t nominal = p.halves == 4 ? NOMINAL_GROUPS / 2 : NOMINAL_GROUPS;
-  int64_t target = ((all_steps + nominal - 1) / nominal + 1) / 2;
+  int64_t target = (all_steps + nominal - 1) / nominal;
   if (target < row_steps) target = row_steps;
   if (target < MIN_CHUNK) target = MIN_CHUNK;
   int nsplit = (int)((p.key_blocks + target - 1) / target);
+  if (nsplit < 2 && p.key_blocks >= 4 * row_steps) nsplit = 2;
   nsplit = nsplit < 1 ? 1 : (nsplit > MAX_SPLIT ? MAX_SPLIT : nsplit);
   p.chunk = (p.key_blocks + nsplit - 1) / nsplit;
   p.nsplit = (p.key_blocks + p.chunk - 1) / p.chunk;

@@ -79,12 +79,14 @@ def _global_chunks(batch, heads, tokens, global_tokens, width, head_dim=128):
 
 
 def test_global_tile_split_plan():
-    # FLUX 2048 px 16-tile K3 (264 key blocks, 128 paired rows of at most 28 entries): three
-    # chunks of 88 blocks
-    assert _global_chunks(1, 24, 16896, 512, 28) == 3
+    # FLUX 2048 px 16-tile K3 (264 key blocks, 128 paired rows of at most 28 entries): two chunks
+    # of 132 blocks, about a workgroup's average work
+    assert _global_chunks(1, 24, 16896, 512, 28) == 2
     # the same rows padded to twice the 64-query width (rows paired on the device without a host
     # sync) still split: one 264-block item per global tile would outlast the ordinary rows
     assert _global_chunks(1, 24, 16896, 512, 52) == 2
+    # 2048 px 4-tile K1 (rows of 75 entries): a sweep shorter than four rows stays whole
+    assert _global_chunks(1, 24, 16896, 512, 75) == 1
     # 1024 px (72 key blocks): chunks never fall below 64 steps' worth of target, so two of 36
     assert _global_chunks(1, 24, 4608, 512, 16) == 2
     assert _global_chunks(1, 24, 4608, 512, 27) == 2
@@ -92,8 +94,8 @@ def test_global_tile_split_plan():
     assert _global_chunks(1, 24, 4608, 512, 72) == 1
     # 4096 px 16-tile K3 (1032 key blocks, width 75): two chunks of 516
     assert _global_chunks(1, 24, 66048, 512, 75) == 2
-    # one head of it: fourteen chunks of 74 (merge_kernel's general path, past four chunks)
-    assert _global_chunks(1, 1, 66048, 512, 75) == 14
+    # one head of it: thirteen chunks of 80 (merge_kernel's general path, past four chunks)
+    assert _global_chunks(1, 1, 66048, 512, 75) == 13
 
 
 def test_pair_rows_rejections():
@@ -138,7 +140,7 @@ def test_paired_ragged_shapes():
     for G, tiles in ((512, 4), (576, 5), (64, 1)):
         N = 16896 + (G - 512)
         ws = lib.hb_attention_workspace_bytes(1, 24, N, 128, G, 28, 64, 1, 1)
-        assert (ws - 256) == 24 * tiles * 3 * per_chunk, (G, ws)  # three chunks of 88 blocks
+        assert (ws - 256) == 24 * tiles * 2 * per_chunk, (G, ws)  # two chunks of 132 blocks
     assert lib.hb_attention_workspace_bytes(1, 24, 16384, 128, 0, 28, 64, 1, 1) == 256
     # N - G an odd multiple of 64 is accepted; N or G off the 64 grid is not
     assert lib.hb_attention_workspace_bytes(1, 24, 16896 - 64, 128, 512, 28, 64, 1, 1) > 256

@@ -118,7 +118,7 @@ def test_paired_4096_sampled_rows(hip_device):
 
 
 def test_paired_4096_one_head_many_chunks(hip_device):
-    """One head at 4096 px: the planner splits each global tile into 14 chunks (more than the
+    """One head at 4096 px: the planner splits each global tile into 13 chunks (more than the
     merge kernel's four-chunk fast path takes, tests/test_capi.py), so the general merge runs;
     global rows against fp32 attention over all keys, and sampled ordinary rows."""
     from hilberta_amd.paired_kernel import paired_attention
@@ -129,7 +129,7 @@ def test_paired_4096_one_head_many_chunks(hip_device):
     phase = 3
     meta = device_paired(oracle_paired(plan, phase), hip_device)
     lse = torch.empty(1, 1, N, dtype=torch.float32, device=hip_device)
-    say("case paired 4096_t16k3 one head, global tiles in 14 chunks")
+    say("case paired 4096_t16k3 one head, global tiles in 13 chunks")
     out = paired_attention(q, k, v, meta, lse=lse)
     torch.cuda.synchronize()
     qf, kf, vf = q.float(), k.float(), v.float()
