@@ -161,3 +161,54 @@ def test_captures_hold_no_memory_after_their_graphs(hip_device):
     for _ in range(4):
         capture_once()
     assert torch.cuda.memory_allocated(hip_device) == before
+
+
+def test_sparse_attention_ragged_graph_replays_match_eager(hip_device):
+    """sparse_attention on a table that pairs only with overhanging halves (an odd row count and
+    a global prefix that is an odd multiple of 64) captured in a HIP graph: the device pairing
+    launch and the paired forward replay bitwise like the eager call, with eager work between
+    replays."""
+    import numpy as np
+
+    from hilberta_amd.sparse_kernel import sparse_attention
+
+    G, rows = 576, 71
+    N = G + 64 * rows
+    T_ = N // 64
+    rng = np.random.default_rng(41)
+    width = G // 64 + 6
+    ids = np.zeros((rows, width), np.int32)
+    counts = np.zeros(rows, np.int32)
+    for r in range(rows):
+        extra = rng.choice(np.arange(G // 64, T_), size=rng.integers(1, 7), replace=False)
+        row = np.concatenate([np.arange(G // 64), np.sort(extra)]).astype(np.int32)
+        ids[r, :len(row)] = row
+        counts[r] = len(row)
+    idd, cnd = torch.from_numpy(ids).to(hip_device), torch.from_numpy(counts).to(hip_device)
+    q, k, v = (x.to(hip_device) for x in A.seeded_qkv(1, 4, N, 128, seed=43))
+    eager_lse = torch.empty(1, 4, N, dtype=torch.float32, device=hip_device)
+    eager = sparse_attention(q, k, v, idd, cnd, global_tokens=G, lse=eager_lse)
+    out = torch.empty_like(q)
+    lse = torch.empty_like(eager_lse)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        sparse_attention(q, k, v, idd, cnd, global_tokens=G, out=out, lse=lse)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    say("case graph: sparse_attention on a ragged table")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        sparse_attention(q, k, v, idd, cnd, global_tokens=G, out=out, lse=lse)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        say(f"case graph ragged: replay {rep}")
+        out.zero_()
+        lse.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep} output"
+        assert torch.equal(lse, eager_lse), f"replay {rep} lse"
+        x = sparse_attention(q, k, v, idd, cnd, global_tokens=G)
+        torch.cuda.synchronize()
+        assert torch.equal(x, eager)

@@ -4,7 +4,9 @@ Two calls in a row, the second with smaller shapes (fewer heads, a shorter seque
 global tiles), each against hb_paired_fwd with a caller workspace on the same inputs: the same
 kernels on the same plan, so the outputs and LSE are equal bit for bit, and both are within the
 suite's tolerance of the fp32 oracle.  The first call splits its global query tiles, so the split
-partials and the merge run out of the static scratch too.
+partials and the merge run out of the static scratch too.  A ragged case follows: tables paired
+on the device from an odd row count with a global prefix that is an odd multiple of 64, so both
+kinds of overhanging half are skipped with the partials in the static scratch.
 """
 
 import ctypes
@@ -74,3 +76,36 @@ def test_noalloc_matches_workspace_entry_point(hip_device):
             s = torch.matmul(qf[:, :, :G], kf.transpose(-1, -2).contiguous()) * D**-0.5
             compare(o_na[:, :, :G], l_na[:, :, :G], torch.matmul(torch.softmax(s, -1), vf),
                     torch.logsumexp(s, -1), f"noalloc {name} global rows")
+
+
+def test_noalloc_ragged_matches_workspace_entry_point(hip_device):
+    import numpy as np
+    from types import SimpleNamespace
+
+    from hilberta_amd._tables import pair_rows_device
+
+    G, rows, heads = 576, 71, 4
+    N = G + 64 * rows
+    T_ = N // 64
+    rng = np.random.default_rng(47)
+    width = G // 64 + 6
+    ids = np.zeros((rows, width), np.int32)
+    counts = np.zeros(rows, np.int32)
+    for r in range(rows):
+        extra = rng.choice(np.arange(G // 64, T_), size=rng.integers(1, 7), replace=False)
+        row = np.concatenate([np.arange(G // 64), np.sort(extra)]).astype(np.int32)
+        ids[r, :len(row)] = row
+        counts[r] = len(row)
+    pid, pfl, pct = pair_rows_device(torch.from_numpy(ids).to(hip_device),
+                                     torch.from_numpy(counts).to(hip_device), T_,
+                                     paired_width=min(2 * width, T_))
+    meta = SimpleNamespace(kv_indices=pid, kv_flags=pfl, kv_counts=pct, global_tokens=G,
+                           key_block_size=64)
+    q, k, v = A.seeded_qkv(1, heads, N, D, seed=29)
+    qd, kd, vd = (x.to(hip_device) for x in (q, k, v))
+    say(f"case noalloc ragged G={G} rows={rows}")
+    need, (o_ws, l_ws), (o_na, l_na) = _both(qd, kd, vd, meta)
+    assert need > 256, "the global tiles must split"
+    assert torch.equal(o_na, o_ws) and torch.equal(l_na, l_ws), "differs from hb_paired_fwd"
+    ref_o, ref_l = A.block_sparse_attention(q, k, v, ids, counts, global_tokens=G)
+    compare(o_na.cpu(), l_na.cpu(), ref_o, ref_l, "noalloc ragged")
