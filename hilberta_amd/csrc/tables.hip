@@ -510,7 +510,8 @@ extern "C" int hb_bits_emit(const uint32_t* bits, int32_t rows, int32_t total_bl
 // aligns them to the end of the sequence), so paired row 0 holds an empty half 0 and row 0 as
 // half 1.  Ids outside [0, T) and entries past a row's count (clamped to width) are ignored.  A
 // union longer than out_width is cut to out_width entries and sets *overflow (when given) to 1.
-constexpr int PAIR_MAX_BLOCKS = 2048;  // key blocks per row the LDS bitmaps cover
+// key blocks per row the LDS bitmaps cover (N up to 2^20 tokens; 16 KiB of LDS per workgroup)
+constexpr int PAIR_MAX_BLOCKS = 16384;
 constexpr int PAIR_WORDS = PAIR_MAX_BLOCKS / 32 + 2;
 __global__ __launch_bounds__(TPB) void pair_rows_kernel(const int32_t* ids, const int32_t* counts,
                                                         int prows, int lead, int width, int T,
@@ -520,7 +521,9 @@ __global__ __launch_bounds__(TPB) void pair_rows_kernel(const int32_t* ids, cons
   __shared__ uint32_t bm[TPB / 64][2][PAIR_WORDS];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int pr = blockIdx.x * (TPB / 64) + w;
-  for (int i = lane; i < 2 * PAIR_WORDS; i += 64) bm[w][i / PAIR_WORDS][i % PAIR_WORDS] = 0u;
+  // only the words this table's key blocks reach (pair_flag reads bit kb * ratio + kh <= T)
+  const int nwords = T / 32 + 2;
+  for (int i = lane; i < 2 * nwords; i += 64) bm[w][i / nwords][i % nwords] = 0u;
   __syncthreads();
   if (pr < prows) {
     for (int h = 0; h < 2; ++h) {
@@ -589,7 +592,8 @@ extern "C" int hb_pair_rows(const int32_t* kv_indices, const int32_t* kv_counts,
 // as pair_metadata (paired_metadata.py:38-51) taken over four query blocks instead of two.  Ids
 // outside [0, T) and entries past a row's count (clamped to width) are ignored; a union longer
 // than out_width is cut to out_width entries and sets *overflow (when given) to 1.
-constexpr int QUAD_WORDS = PAIR_MAX_BLOCKS / 4;  // four flag bytes per word
+constexpr int QUAD_MAX_BLOCKS = 2048;            // key blocks per row of a quad table
+constexpr int QUAD_WORDS = QUAD_MAX_BLOCKS / 4;  // four flag bytes per word
 __global__ __launch_bounds__(TPB) void quad_rows_kernel(const int32_t* ids, const int32_t* flags,
                                                         const int32_t* counts, int qrows, int width,
                                                         int T, int group, int out_width,
@@ -651,8 +655,8 @@ extern "C" int hb_quad_rows(const int32_t* kv_indices, const int32_t* kv_flags,
   HB_REQUIRE(rows > 0 && rows % group == 0,
              "rows must be a positive multiple of %d (got %d)", group, rows);
   HB_REQUIRE(width > 0 && quad_width > 0, "table widths must be positive");
-  HB_REQUIRE(total_blocks > 0 && total_blocks <= PAIR_MAX_BLOCKS,
-             "total_blocks must be in [1, %d] (got %d)", PAIR_MAX_BLOCKS, total_blocks);
+  HB_REQUIRE(total_blocks > 0 && total_blocks <= QUAD_MAX_BLOCKS,
+             "total_blocks must be in [1, %d] (got %d)", QUAD_MAX_BLOCKS, total_blocks);
   const int qrows = rows / group, per_block = TPB / 64;
   hipLaunchKernelGGL(quad_rows_kernel, dim3((qrows + per_block - 1) / per_block), dim3(TPB), 0,
                      stream, kv_indices, kv_flags, kv_counts, qrows, width, total_blocks, group,

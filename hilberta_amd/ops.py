@@ -29,6 +29,8 @@ from . import _lib
 from ._workspace import attention_workspace
 
 _NS = "hilberta_hip"
+# key blocks per row hb_pair_rows pairs (include/hilberta_hip.h)
+PAIR_MAX_BLOCKS = 16384
 
 
 def _strides(q, k, v, out):
@@ -71,7 +73,7 @@ def sparse_fwd(q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: Optional[Tenso
                all_queries: bool, num_groups: int) -> None:
     """Unpaired 64-query tables (replaces the _block_sparse_fwd launch, sparse_kernel.py:315-339).
 
-    With at most 2048 key blocks, rows 2r, 2r + 1 are merged on the device by hb_pair_rows, as
+    With at most PAIR_MAX_BLOCKS key blocks, rows 2r, 2r + 1 are merged on the device by hb_pair_rows, as
     pair_metadata does (paired_metadata.py:26-51), and run on hb_paired_fwd: a 128-query item
     keeps two waves per SIMD busy where a 64-query item keeps one (1.7-1.85x faster).  An odd row
     count is paired from the end, its first paired row carrying an empty half that reaches into
@@ -84,7 +86,7 @@ def sparse_fwd(q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: Optional[Tenso
     B, H, N, D = q.shape
     blocks = N // 64
     stream = _lib.stream_ptr(q.device)
-    if blocks <= 2048:
+    if blocks <= PAIR_MAX_BLOCKS:
         width = min(2 * kv_indices.shape[1], blocks)
         ids, flags, counts = pair_rows(kv_indices, kv_counts, blocks, 64, width)
         ws = attention_workspace(q.device, B, H, N, D, global_tokens, width, 64, paired=1,

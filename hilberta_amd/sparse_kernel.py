@@ -201,7 +201,7 @@ def _block_sparse_fwd(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, s
                       all_queries):
     """Launch through the operator hilberta_hip::sparse_fwd on the current stream (module-level
     so tests can patch it).  The rows are paired on the device (an odd row count from the end)
-    and run on the paired kernel up to 2048 key blocks; see hilberta_amd.ops.sparse_fwd."""
+    and run on the paired kernel up to 16384 key blocks; see hilberta_amd.ops.sparse_fwd."""
     from . import ops
 
     ops.sparse_fwd(q, k, v, out, lse, kv_indices, kv_counts, int(global_tokens), float(scale_log2),

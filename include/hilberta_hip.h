@@ -222,7 +222,7 @@ int hb_bits_emit(const uint32_t* bits, int32_t rows, int32_t total_blocks, int32
  * hb_paired_fwd expects for ordinary query counts that are odd multiples of 64; pair_metadata
  * itself rejects odd counts).  paired_width should bound every paired row's entries
  * (min(2*width, key blocks) always does): a longer row is cut to paired_width entries and sets
- * *overflow (device int32, may be NULL; never cleared here) to 1.  total_blocks <= 2048.  No host
+ * *overflow (device int32, may be NULL; never cleared here) to 1.  total_blocks <= 16384.  No host
  * synchronisation. */
 int hb_pair_rows(const int32_t* kv_indices, const int32_t* kv_counts, int32_t rows, int32_t width,
                  int32_t total_blocks, int32_t key_block_size, int32_t* paired_ids,

@@ -103,7 +103,10 @@ def test_pair_rows_rejections():
     buf = ctypes.c_void_p(16)  # never dereferenced: every call below fails its argument checks
     rc = lib.hb_pair_rows(buf, buf, 0, 4, 72, 64, buf, buf, buf, 8, None, None)
     assert rc == 1 and "rows must be positive" in _lib.last_error()
-    rc = lib.hb_pair_rows(buf, buf, 4, 4, 4096, 64, buf, buf, buf, 8, None, None)
+    rc = lib.hb_pair_rows(buf, buf, 4, 4, 16385, 64, buf, buf, buf, 8, None, None)
+    assert rc == 1 and "total_blocks" in _lib.last_error()
+    # quad rows keep 2048 key blocks
+    rc = lib.hb_quad_rows(buf, buf, buf, 4, 8, 4096, buf, buf, buf, 8, None, None)
     assert rc == 1 and "total_blocks" in _lib.last_error()
     rc = lib.hb_pair_rows(buf, buf, 4, 4, 72, 96, buf, buf, buf, 8, None, None)
     assert rc == 1 and "key_block_size" in _lib.last_error()

@@ -204,6 +204,29 @@ def test_ragged_tables_run_paired(hip_device, G, rows, dim):
         assert torch.equal(lse[:, :, G:], ul[:, :, G:]), "ordinary LSE differs from the unpaired kernel"
 
 
+def test_long_ragged_table_runs_paired(hip_device):
+    """A ragged table of 4008 key blocks (beyond the old 2048-block pairing limit, N = 256448):
+    sparse_attention pairs it on the device; its ordinary rows equal the 64-query kernel's bit for
+    bit and its global rows match fp32 attention over every key."""
+    from hilberta_amd.sparse_kernel import sparse_attention
+
+    G, rows, dim = 576, 3999, 64
+    N = G + 64 * rows
+    ids, counts = _random_rows(G, rows, seed=61)
+    q, k, v = (x.to(hip_device) for x in A.seeded_qkv(1, 1, N, dim, seed=62))
+    idd, cnd = torch.from_numpy(ids).to(hip_device), torch.from_numpy(counts).to(hip_device)
+    say(f"case long ragged table N={N} D={dim}")
+    lse = torch.empty(1, 1, N, dtype=torch.float32, device=hip_device)
+    out = sparse_attention(q, k, v, idd, cnd, global_tokens=G, lse=lse)
+    uo, ul = _unpaired_kernel(q, k, v, idd, cnd, G, dim ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(out[:, :, G:], uo[:, :, G:]), "ordinary rows differ from the unpaired kernel"
+    assert torch.equal(lse[:, :, G:], ul[:, :, G:]), "ordinary LSE differs from the unpaired kernel"
+    s = torch.matmul(q[:, :, :G].float(), k.float().transpose(-1, -2).contiguous()) * dim ** -0.5
+    compare(out[:, :, :G], lse[:, :, :G], torch.matmul(torch.softmax(s, -1), v.float()),
+            torch.logsumexp(s, -1), "long ragged global rows")
+
+
 @pytest.mark.parametrize("dtype,dim", [(torch.float16, 128), (torch.bfloat16, 64), (torch.float16, 64)])
 def test_dtypes_and_head_dim(hip_device, dtype, dim):
     from hilberta_amd.paired_kernel import paired_attention

@@ -318,3 +318,33 @@ def test_pair_rows_reports_overflow(hip_device):
         assert np.array_equal(pct.cpu().numpy(), np.minimum(ref_counts, width))
         assert np.array_equal(pid.cpu().numpy()[:, :width][ref_counts >= width],
                               np.asarray(ref["kv_indices"])[ref_counts >= width, :width])
+
+
+def test_pair_rows_beyond_2048_key_blocks(hip_device):
+    """Tables of more than 2048 key blocks pair on the device too (up to 16384): random rows over
+    4008 key blocks, bit-exact with pair_metadata."""
+    from hilberta_amd._tables import pair_rows_device
+
+    G, rows = 512, 4000
+    N = G + 64 * rows
+    T_ = N // 64
+    rng = np.random.default_rng(17)
+    width = G // 64 + 10
+    ids = np.zeros((rows, width), np.int32)
+    counts = np.zeros(rows, np.int32)
+    for r in range(rows):
+        extra = rng.choice(np.arange(G // 64, T_), size=rng.integers(1, 11), replace=False)
+        row = np.concatenate([np.arange(G // 64), np.sort(extra)]).astype(np.int32)
+        ids[r, :len(row)] = row
+        counts[r] = len(row)
+    ref = T.pair_metadata(ids, counts, tokens=N, global_tokens=G)
+    say(f"case pair_rows T={T_}")
+    pid, pfl, pct = pair_rows_device(torch.from_numpy(ids).to(hip_device),
+                                     torch.from_numpy(counts).to(hip_device), T_,
+                                     paired_width=2 * width)
+    torch.cuda.synchronize()
+    pid, pfl, pct = pid.cpu().numpy(), pfl.cpu().numpy(), pct.cpu().numpy()
+    rw = ref["kv_indices"].shape[1]
+    assert np.array_equal(pct, ref["kv_counts"])
+    assert np.array_equal(pid[:, :rw], ref["kv_indices"]) and np.array_equal(pfl[:, :rw], ref["kv_flags"])
+    assert not pid[:, rw:].any() and not pfl[:, rw:].any()
