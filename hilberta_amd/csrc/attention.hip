@@ -55,8 +55,9 @@ constexpr int MAX_SPLIT = 16;  // chunks per global query tile, at most
 constexpr int NOMINAL_GROUPS = 512;  // persistent workgroups on a full MI355X (2 per CU)
 constexpr int MIN_CHUNK = 64;  // key-block steps per global chunk, at least (shorter chunks' fixed costs show)
 // V operands (ds_read_b64_tr_b16 pairs) in flight ahead of the PV MFMAs: three cover the LDS
-// latency under load better than two (2-3 % at 2048 px 16-tile K3, bitwise-identical results)
-constexpr int PFV = 3;
+// latency under load better than two (2-3 % at 2048 px 16-tile K3), four a little better again
+// (0.2-1 % at every configuration, no spills; bitwise-identical results)
+constexpr int PFV = 4;
 // word 3 of a raw buffer resource (32-bit data format, no swizzle), as for gfx9-family buffers
 constexpr int BUFFER_WORD3 = 0x00020000;
 // __builtin_amdgcn_sched_group_barrier instruction classes
