@@ -76,6 +76,16 @@ SIGNATURES = {
         _c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p, _p, _p, _p, _p, _p],
     ),
     "hb_paired_plan_emit": (_c_int, [_c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p, _p, _p]),
+    "hb_hilbert_order_host": (_c_int, [_c_int, _p]),
+    "hb_plan_layout_host": (_c_int, [_c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p, _p, _p, _p]),
+    "hb_plan_phase_bits_host": (
+        _c_int,
+        [_p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p, _p],
+    ),
+    "hb_table_bits_host": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _p]),
+    "hb_bits_counts_host": (_c_int, [_p, _c_int, _c_int, _c_int, _p, _p, _p]),
+    "hb_bits_emit_host": (_c_int, [_p, _c_int, _c_int, _c_int, _p, _c_int, _p, _p, _c_int]),
+    "hb_pair_rows_host": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _c_int, _p]),
 }
 
 _lib = None

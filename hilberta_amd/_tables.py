@@ -1,8 +1,11 @@
-"""Drives the HIP block-table builder (csrc/tables.hip) through the C ABI.
+"""Drives the block-table builder through the C ABI: the HIP kernels of csrc/tables.hip on a
+GPU, or their host counterparts (csrc/tables_host.hip, the ``*_host`` entry points, bit-identical)
+when the caller asks for ``device="cpu"``.
 
-All integer work runs on the GPU.  The only host synchronisations are the ones the table format
-forces at setup time: the number of shared blocks of the layout (it sizes the global prefix) and
-the widest row of each emitted table (it is the table width).
+On the GPU all integer work runs on the device.  The only host synchronisations are the ones the
+table format forces at setup time: the number of shared blocks of the layout (it sizes the global
+prefix) and the widest row of each emitted table (it is the table width).  The host builder is
+for plan setup on machines without a GPU; the attention kernels have no host path.
 """
 
 from __future__ import annotations
@@ -15,12 +18,27 @@ from . import _lib
 
 
 def _dev(device):
+    """The device tables are built on: ``None`` is the current HIP device; ``"cpu"`` selects the
+    host builder explicitly (it is never chosen in place of a GPU)."""
     if device is None:
+        if not torch.cuda.is_available():
+            raise RuntimeError("no HIP device: pass device='cpu' to build the tables on the host")
         return torch.device("cuda", torch.cuda.current_device())
     device = torch.device(device)
-    if device.type != "cuda":
-        raise ValueError("the table builder runs on a HIP device (cuda:N); there is no CPU path")
+    if device.type not in ("cuda", "cpu"):
+        raise ValueError("the table builder runs on a HIP device (cuda:N) or on the host (cpu)")
     return device
+
+
+def _run(device, name, *args):
+    """Call entry point ``name`` on ``device``: the HIP launch on the current stream, or its
+    ``_host`` counterpart (no stream argument) for CPU tensors."""
+    lib = _lib.load()
+    if device.type == "cpu":
+        rc = getattr(lib, name + "_host")(*args)
+    else:
+        rc = getattr(lib, name)(*args, _lib.stream_ptr(device))
+    _lib.check(rc, name)
 
 
 @dataclass
@@ -70,22 +88,19 @@ class DeviceLayout:
 def hilbert_order_device(grid_size, device=None):
     device = _dev(device)
     out = torch.empty(grid_size * grid_size, dtype=torch.int64, device=device)
-    _lib.check(_lib.load().hb_hilbert_order(grid_size, out.data_ptr(), _lib.stream_ptr(device)),
-               "hb_hilbert_order")
+    _run(device, "hb_hilbert_order", grid_size, out.data_ptr())
     return out
 
 
 def layout_device(grid_size, block_size, text_tokens, shared, device=None):
     device = _dev(device)
-    lib = _lib.load()
     n = grid_size * grid_size
     nb = n // block_size
     i64 = dict(dtype=torch.int64, device=device)
     t = [torch.empty(n, **i64) for _ in range(4)] + [torch.empty(nb, **i64) for _ in range(2)]
     status = torch.zeros(3, dtype=torch.int32, device=device)
-    rc = lib.hb_plan_layout(grid_size, block_size, text_tokens, int(bool(shared)),
-                            *[x.data_ptr() for x in t], status.data_ptr(), _lib.stream_ptr(device))
-    _lib.check(rc, "hb_plan_layout")
+    _run(device, "hb_plan_layout", grid_size, block_size, text_tokens, int(bool(shared)),
+         *[x.data_ptr() for x in t], status.data_ptr())
     # setup-time sync: the prefix length is data dependent; the same read checks that the image
     # order is a permutation, so the per-forward gathers may trust it
     n_shared, partial, bad_order = status.tolist()
@@ -99,20 +114,16 @@ def layout_device(grid_size, block_size, text_tokens, shared, device=None):
 def phase_bits_device(layout: DeviceLayout, tile_count, phase, bridge_mode, k, scratch=None):
     """Adjacency bitmap [ordinary, words] (int32 storage of uint32 words) and chosen bridges [nb, k]."""
     device = layout.original_order.device
-    lib = _lib.load()
     kk = max(int(k), 1)
     bits = torch.empty((layout.ordinary_blocks, layout.words), dtype=torch.int32, device=device)
     chosen = torch.full((layout.image_blocks, kk), -1, dtype=torch.int64, device=device)
     if bridge_mode and scratch is None:
         scratch = torch.empty(layout.image_blocks**2, dtype=torch.int32, device=device)
-    rc = lib.hb_plan_phase_bits(
-        layout.inverse_original.data_ptr(), layout.physical_original_blocks.data_ptr(),
-        layout.original_to_physical.data_ptr(), layout.grid_size, tile_count, layout.text_tokens,
-        layout.block_size, layout.shared_blocks, phase, bridge_mode, kk,
-        scratch.data_ptr() if bridge_mode else None, chosen.data_ptr(), bits.data_ptr(),
-        _lib.stream_ptr(device),
-    )
-    _lib.check(rc, "hb_plan_phase_bits")
+    _run(device, "hb_plan_phase_bits",
+         layout.inverse_original.data_ptr(), layout.physical_original_blocks.data_ptr(),
+         layout.original_to_physical.data_ptr(), layout.grid_size, tile_count, layout.text_tokens,
+         layout.block_size, layout.shared_blocks, phase, bridge_mode, kk,
+         scratch.data_ptr() if bridge_mode else None, chosen.data_ptr(), bits.data_ptr())
     return bits, chosen
 
 
@@ -124,11 +135,9 @@ def _bits_counts(bits, total_blocks, unpaired, paired, key_block_size):
     counts = torch.empty(rows, **i32) if unpaired else None
     pcounts = torch.empty(rows // 2, **i32) if paired else None
     maxc = torch.zeros(2, **i32)
-    rc = _lib.load().hb_bits_counts(bits.data_ptr(), rows, total_blocks, key_block_size,
-                                    counts.data_ptr() if unpaired else None,
-                                    pcounts.data_ptr() if paired else None, maxc.data_ptr(),
-                                    _lib.stream_ptr(device))
-    _lib.check(rc, "hb_bits_counts")
+    _run(device, "hb_bits_counts", bits.data_ptr(), rows, total_blocks, key_block_size,
+         counts.data_ptr() if unpaired else None, pcounts.data_ptr() if paired else None,
+         maxc.data_ptr())
     return counts, pcounts, maxc
 
 
@@ -141,12 +150,9 @@ def _bits_emit(bits, total_blocks, counts, pcounts, width, pwidth, unpaired, pai
     ids = torch.empty((rows, width), **i32) if unpaired else None
     pids = torch.empty((rows // 2, pwidth), **i32) if paired else None
     pflags = torch.empty((rows // 2, pwidth), **i32) if paired else None
-    rc = _lib.load().hb_bits_emit(bits.data_ptr(), rows, total_blocks, key_block_size,
-                                  ids.data_ptr() if unpaired else None, width,
-                                  pids.data_ptr() if paired else None,
-                                  pflags.data_ptr() if paired else None, pwidth,
-                                  _lib.stream_ptr(device))
-    _lib.check(rc, "hb_bits_emit")
+    _run(device, "hb_bits_emit", bits.data_ptr(), rows, total_blocks, key_block_size,
+         ids.data_ptr() if unpaired else None, width, pids.data_ptr() if paired else None,
+         pflags.data_ptr() if paired else None, pwidth)
     out = {}
     if unpaired:
         out.update(kv_indices=ids, kv_counts=counts)
@@ -185,14 +191,24 @@ def emit_device_many(bits_list, total_blocks, *, unpaired=True, paired=False, ke
     ]
 
 
+def _check_table(kv_indices, kv_counts):
+    """The entry points read ``kv_indices`` as int32 [rows, width] and ``kv_counts`` as int32
+    [rows], contiguous, on one device."""
+    if (kv_indices.dtype != torch.int32 or kv_counts.dtype != torch.int32 or kv_indices.dim() != 2
+            or kv_counts.shape != (kv_indices.shape[0],) or not kv_indices.is_contiguous()
+            or not kv_counts.is_contiguous() or kv_indices.device != kv_counts.device):
+        raise ValueError("tables must be contiguous int32 kv_indices [rows, width] and kv_counts "
+                         "[rows] on one device")
+
+
 def table_bits_device(kv_indices, kv_counts, total_blocks):
+    _check_table(kv_indices, kv_counts)
     device = kv_indices.device
     rows, width = kv_indices.shape
     words = (total_blocks + 31) // 32
     bits = torch.empty((rows, words), dtype=torch.int32, device=device)
-    rc = _lib.load().hb_table_bits(kv_indices.data_ptr(), kv_counts.data_ptr(), rows, width,
-                                   total_blocks, bits.data_ptr(), _lib.stream_ptr(device))
-    _lib.check(rc, "hb_table_bits")
+    _run(device, "hb_table_bits", kv_indices.data_ptr(), kv_counts.data_ptr(), rows, width,
+         total_blocks, bits.data_ptr())
     return bits
 
 
@@ -206,20 +222,18 @@ def pair_rows_device(kv_indices, kv_counts, total_blocks, *, key_block_size=64, 
     ``paired_width``, which should bound every paired row's entry count (min(2 * width, key
     blocks) always does).  ``overflow`` may be a device int32 scalar tensor that is set to 1 when
     some paired row had to be cut to ``paired_width`` entries.  Returns (ids, flags, counts) as
-    int32 device tensors.
+    int32 device tensors.  CPU tables are paired on the host (hb_pair_rows_host).
     """
+    _check_table(kv_indices, kv_counts)
     device = kv_indices.device
     rows, width = kv_indices.shape
     prows = (rows + 1) // 2
     ids = torch.empty((prows, paired_width), dtype=torch.int32, device=device)
     flags = torch.empty_like(ids)
     counts = torch.empty((prows,), dtype=torch.int32, device=device)
-    rc = _lib.load().hb_pair_rows(kv_indices.data_ptr(), kv_counts.data_ptr(), rows, width,
-                                  total_blocks, key_block_size, ids.data_ptr(), flags.data_ptr(),
-                                  counts.data_ptr(), paired_width,
-                                  overflow.data_ptr() if overflow is not None else None,
-                                  _lib.stream_ptr(device))
-    _lib.check(rc, "hb_pair_rows")
+    _run(device, "hb_pair_rows", kv_indices.data_ptr(), kv_counts.data_ptr(), rows, width,
+         total_blocks, key_block_size, ids.data_ptr(), flags.data_ptr(), counts.data_ptr(),
+         paired_width, overflow.data_ptr() if overflow is not None else None)
     return ids, flags, counts
 
 
@@ -257,11 +271,15 @@ def paired_plan_tables_device(grid_size, tile_count, k, text_tokens, shared, key
     and one host read (hb_paired_plan_tables / hb_paired_plan_emit).
 
     Returns (DeviceLayout, [(ids, flags, counts) per phase]) on the device.  The host read takes the
-    shared-prefix length, the layout checks and the four table widths at once.
+    shared-prefix length, the layout checks and the four table widths at once.  With
+    ``device="cpu"`` the same tables come from the host builder (_paired_plan_tables_host).
     """
     import ctypes
 
     device = _dev(device)
+    if device.type == "cpu":
+        return _paired_plan_tables_host(grid_size, tile_count, k, text_tokens, shared,
+                                        key_block_size)
     lib = _lib.load()
     n = grid_size * grid_size
     nb = n // 64
@@ -303,3 +321,17 @@ def paired_plan_tables_device(grid_size, tile_count, k, text_tokens, shared, key
                                  ptrs(0), ptrs(1), ptrs(2), (ctypes.c_int32 * 4)(*widths), stream)
     _lib.check(rc, "hb_paired_plan_emit")
     return layout, tables
+
+
+def _paired_plan_tables_host(grid_size, tile_count, k, text_tokens, shared, key_block_size):
+    """paired_plan_tables_device on the host: the layout, each phase's reciprocal top-K bitmap and
+    its paired tables from the host entry points, the steps the fused device plan runs."""
+    cpu = torch.device("cpu")
+    layout = layout_device(grid_size, 64, text_tokens, shared, cpu)
+    if layout.ordinary_blocks % 2:
+        raise ValueError("Paired queries require N/global aligned to 128; KV must be 64/128")
+    scratch = torch.empty(layout.image_blocks**2, dtype=torch.int32)
+    bits = [phase_bits_device(layout, tile_count, phase, 2, k, scratch)[0] for phase in range(4)]
+    tables = emit_device_many(bits, layout.total_blocks, unpaired=False, paired=True,
+                              key_block_size=key_block_size)
+    return layout, [(t["paired_indices"], t["paired_flags"], t["paired_counts"]) for t in tables]

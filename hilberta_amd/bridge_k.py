@@ -3,9 +3,10 @@
 ``bridge_k_plan`` keeps the reference's signature and results (bridge_k.py:10-51): per phase,
 every query block takes its K best key blocks by (-score, (key - offset/64) mod nb), where the
 score counts cross-tile 4-neighbour token pairs between the two blocks, and the block adjacency is
-closed under transposition.  The tables are built on the GPU (csrc/tables.hip, bridge mode 2)
-and returned on the CPU.  ``paired_plan_device`` is the all-device fast path: it emits the four
-phases' paired tables straight from the adjacency bitmaps, ready for ``paired_attention``.
+closed under transposition.  The tables are built on the GPU (csrc/tables.hip, bridge mode 2),
+or on the host with ``device="cpu"`` (csrc/tables_host.hip), and returned on the CPU.
+``paired_plan_device`` is the all-device fast path: it emits the four phases' paired tables
+straight from the adjacency bitmaps, ready for ``paired_attention``.
 """
 
 from __future__ import annotations
@@ -52,7 +53,8 @@ class DevicePlan:
 def paired_plan_device(tiles=4, k=1, shared=False, *, grid_size=64, text_tokens=512,
                        key_block_size=64, device=None):
     """bridge_k_plan + pair_metadata for all four phases without leaving the GPU: six launches and
-    one host read (_tables.paired_plan_tables_device)."""
+    one host read (_tables.paired_plan_tables_device).  ``device="cpu"`` builds the same tables
+    on the host."""
     _check_k(k)
     tiles, grid_size, text_tokens, block_size = _check_geometry(tiles, grid_size, text_tokens, 64)
     if key_block_size not in (64, 128) or (text_tokens + grid_size**2) % 128:

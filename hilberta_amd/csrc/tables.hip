@@ -17,34 +17,13 @@
 //
 // Integer atomics only (order-independent sums and ORs), so results do not depend on scheduling.
 #include "common.h"
+#include "tables_common.h"
 #include "../../include/hilberta_hip.h"
 
 namespace hb {
 namespace {
 
 constexpr int TPB = 256;
-
-__device__ __forceinline__ int64_t hilbert_raster(int64_t d, int g) {
-  // geometry.py:6-25: d2xy with the quadrant rotation, then raster id (g-1-y)*g + x
-  int64_t x = 0, y = 0, t = d;
-  for (int s = 1; s < g; s *= 2) {
-    const int64_t rx = (t / 2) & 1;
-    const int64_t ry = (t ^ (t / 2)) & 1;
-    if (ry == 0) {
-      if (rx) {
-        x = s - 1 - x;
-        y = s - 1 - y;
-      }
-      const int64_t tmp = x;
-      x = y;
-      y = tmp;
-    }
-    x += s * rx;
-    y += s * ry;
-    t /= 4;
-  }
-  return (int64_t)(g - 1 - y) * g + x;
-}
 
 __global__ void hilbert_kernel(int g, int64_t* out) {
   const int64_t n = (int64_t)g * g;
@@ -152,10 +131,6 @@ __global__ void order_check_kernel(int64_t n, const int64_t* order, const int64_
 __global__ void zero_kernel(uint32_t* p, int64_t words) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < words; i += (int64_t)gridDim.x * blockDim.x)
     p[i] = 0;
-}
-
-__device__ __forceinline__ int tile_label(int64_t pos, int64_t off, int64_t n, int64_t width) {
-  return (int)((((pos - off) % n) + n) % n / width);
 }
 
 // scores[qa*nb + qc] += 1 and [qc*nb + qa] += 1 for every 4-neighbour raster pair (a, c) whose
@@ -279,20 +254,6 @@ __global__ void table_bits_kernel(const int32_t* ids, const int32_t* counts, int
     if (p < 0 || p >= T) continue;  // tables are validated on the host; never write out of range
     atomicOr(&bits[(int64_t)r * words + p / 32], 1u << (p % 32));
   }
-}
-
-// Merged word of paired row pr for key-block granularity ratio (1: 64-token keys, 2: 128-token):
-// returns the union mask over key blocks covered by 32*ratio physical ids starting at word w*ratio,
-// computed lazily per key block below.
-__device__ __forceinline__ int pair_flag(const uint32_t* ra, const uint32_t* rb, int kb, int ratio) {
-  int flag = 0;
-  for (int kh = 0; kh < ratio; ++kh) {
-    const int p = kb * ratio + kh;
-    const uint32_t a = (ra[p / 32] >> (p % 32)) & 1u;
-    const uint32_t b = (rb[p / 32] >> (p % 32)) & 1u;
-    flag |= (int)(a << (2 * kh)) | (int)(b << (1 + 2 * kh));
-  }
-  return flag;
 }
 
 // Counts: one wave per row.  mode 0: unpaired rows (popcount); mode 1: paired rows at ratio.

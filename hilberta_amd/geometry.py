@@ -1,7 +1,8 @@
 """Hilbert ordering and grid neighbours (drop-in for reference hilberta/geometry.py).
 
 ``hilbert_order`` is computed on the GPU (hb_hilbert_order: d2xy Hilbert then a vertical flip to
-raster ids (g-1-y)*g + x, geometry.py:6-25) and returned on the CPU like the reference's.
+raster ids (g-1-y)*g + x, geometry.py:6-25), or on the host with ``device="cpu"``
+(hb_hilbert_order_host), and returned on the CPU like the reference's.
 ``neighbor_pairs`` is host bookkeeping (the device builder enumerates the same pairs inside its
 score kernel): ascending undirected 4/8-neighbour pairs, row-major, right then down (then the two
 diagonals), geometry.py:28-43.

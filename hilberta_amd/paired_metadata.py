@@ -2,12 +2,13 @@
 
 Drop-in for reference hilberta/paired_metadata.py.  ``PairedMetadata`` is the same frozen
 carrier (paired_metadata.py:8-23).  ``pair_metadata`` keeps its signature and CPU validation
-(validate_metadata) but does the merge itself on the GPU with the HIP table kernels (the rows
-become adjacency bitmaps, hb_table_bits; paired rows are counted and emitted from them,
-hb_bits_counts / hb_bits_emit): for paired row r the key blocks of query blocks 2r and 2r+1 are unioned in ascending block
-order and each key block gets flag bit (half + 2*key_half) for every (query half, 64-key half)
-that sees it (paired_metadata.py:26-51).  Tables come back on the CPU, as in the reference, so
-callers keep their own ``.to(device)`` caching; ``pair_metadata_device`` keeps them on the GPU.
+(validate_metadata) but does the merge itself with the table builder, on the GPU by default or on
+the host with ``device="cpu"`` (the rows become adjacency bitmaps, hb_table_bits; paired rows are
+counted and emitted from them, hb_bits_counts / hb_bits_emit): for paired row r the key blocks of
+query blocks 2r and 2r+1 are unioned in ascending block order and each key block gets flag bit
+(half + 2*key_half) for every (query half, 64-key half) that sees it (paired_metadata.py:26-51).
+Tables come back on the CPU, as in the reference, so callers keep their own ``.to(device)``
+caching; ``pair_metadata_device`` keeps them where they were built.
 """
 
 from __future__ import annotations
@@ -16,8 +17,7 @@ from dataclasses import dataclass, replace
 
 import torch
 
-from . import _lib
-from ._tables import emit_device, table_bits_device
+from ._tables import _dev, emit_device, table_bits_device
 from .sparse_kernel import validate_metadata
 
 
@@ -40,13 +40,13 @@ class PairedMetadata:
 
 
 def pair_tables_device(kv_indices, kv_counts, *, tokens, key_block_size):
-    """Pair validated int32 tables already on the GPU; returns (ids, flags, counts) on the GPU.
+    """Pair validated int32 tables on one device (a GPU, or the CPU for the host builder);
+    returns (ids, flags, counts) on that device.
 
     The rows become adjacency bitmaps (hb_table_bits), paired rows are emitted in ascending key
-    block order (hb_bits_counts / hb_bits_emit).  One host synchronisation reads the widest paired
-    row, which fixes the table width.
+    block order (hb_bits_counts / hb_bits_emit).  On a GPU one host synchronisation reads the
+    widest paired row, which fixes the table width.
     """
-    _lib.require_gpu(kv_indices, kv_counts)
     total_blocks = tokens // 64
     bits = table_bits_device(kv_indices.contiguous(), kv_counts.contiguous(), total_blocks)
     out = emit_device(bits, total_blocks, unpaired=False, paired=True, key_block_size=key_block_size)
@@ -59,7 +59,8 @@ def pair_metadata(kv_indices, kv_counts, *, tokens, global_tokens=768, key_block
     KV64 flags bits 0/1 correspond to query half 0/1.  KV128 adds bits 2/3 for query halves 0/1
     attending the block's second 64-token key half.  No key is duplicated.  All work happens once
     at plan setup, never inside attention.  The merge runs on ``device`` (default: the current
-    HIP device); the result is returned on the CPU like the reference's.
+    HIP device; ``"cpu"``: the host builder); the result is returned on the CPU like the
+    reference's.
     """
     validate_metadata(kv_indices, kv_counts, tokens=tokens, global_tokens=global_tokens)
     if key_block_size not in (64, 128) or tokens % 128 or global_tokens % 128:
@@ -73,14 +74,16 @@ def pair_metadata(kv_indices, kv_counts, *, tokens, global_tokens=768, key_block
 
 def pair_metadata_device(kv_indices, kv_counts, *, tokens, global_tokens=768, key_block_size=64,
                          device=None, validated=False):
-    """As pair_metadata, but the tables stay on the GPU (ready for paired_attention)."""
+    """As pair_metadata, but the tables stay on ``device`` (on a GPU, ready for
+    paired_attention)."""
     if not validated:
         validate_metadata(kv_indices, kv_counts, tokens=tokens, global_tokens=global_tokens)
         if key_block_size not in (64, 128) or tokens % 128 or global_tokens % 128:
             raise ValueError("Paired queries require N/global aligned to 128; KV must be 64/128")
-    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    device = _dev(device)
     ids, flags, counts = pair_tables_device(
-        kv_indices.to(device), kv_counts.to(device), tokens=tokens, key_block_size=key_block_size
+        kv_indices.to(device).contiguous(), kv_counts.to(device).contiguous(), tokens=tokens,
+        key_block_size=key_block_size,
     )
     return PairedMetadata(ids, flags, counts, int(tokens), int(global_tokens), int(key_block_size))
 

@@ -3,8 +3,9 @@
 Physical stream is [text, shared image blocks, remaining image blocks].  Tile membership and
 bridge tie breaking use the ORIGINAL phase ordering.  ``PhasePlan`` / ``AttentionPlan`` are the
 reference's carriers (plan.py:17-111).  ``build_plan`` keeps its signature, validation and
-results (plan.py:114-197) but the tables are built on the GPU by csrc/tables.hip and returned on
-the CPU; ``full_attention_plan`` (plan.py:200-212) is host bookkeeping.
+results (plan.py:114-197) but the tables are built on the GPU by csrc/tables.hip (or on the host
+by csrc/tables_host.hip with ``device="cpu"``) and returned on the CPU; ``full_attention_plan``
+(plan.py:200-212) is host bookkeeping.
 """
 
 from __future__ import annotations
@@ -154,7 +155,8 @@ def _device_plan(tile_count, grid_size, text_tokens, shared, bridge_mode, k, blo
 
 def build_plan(tile_count=4, grid_size=64, text_tokens=512, shared=True, bridge=True, block_size=64,
                *, device=None):
-    """Build the static plan on the GPU; the returned AttentionPlan holds CPU tensors."""
+    """Build the static plan on ``device`` (default: the current HIP device; ``"cpu"``: the host
+    builder); the returned AttentionPlan holds CPU tensors."""
     tile_count, grid_size, text_tokens, block_size = _check_geometry(
         tile_count, grid_size, text_tokens, block_size
     )

@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define HB_ABI_VERSION 3
+#define HB_ABI_VERSION 4
 #define HB_DTYPE_BF16 0
 #define HB_DTYPE_F16 1
 
@@ -263,6 +263,36 @@ int hb_quad_rows(const int32_t* kv_indices, const int32_t* kv_flags, const int32
                  int32_t rows, int32_t width, int32_t total_blocks, int32_t* quad_ids,
                  int32_t* quad_flags, int32_t* quad_counts, int32_t quad_width, int32_t* overflow,
                  hb_stream_t stream);
+
+/* ---------------------------------------------------------------- (b) block tables on the host
+ * The table builder on the CPU, for callers that set plans up on a host without a GPU (the
+ * reference builds every table there: hilberta/geometry.py:6-25, plan.py:114-197,
+ * bridge_k.py:10-51, paired_metadata.py:26-51).  Each takes the arguments of the device entry
+ * point of the same name without the _host suffix, minus the stream, as host pointers, with the
+ * same checks and error codes, and writes the same values bit for bit; it runs synchronously on
+ * the calling thread and makes no HIP call.  The attention launches have no host counterpart. */
+int hb_hilbert_order_host(int32_t grid_size, int64_t* out);
+int hb_plan_layout_host(int32_t grid_size, int32_t block_size, int32_t text_tokens, int32_t shared,
+                        int64_t* original_order, int64_t* inverse_original, int64_t* image_order,
+                        int64_t* inverse_image_order, int64_t* physical_original_blocks,
+                        int64_t* original_to_physical, int32_t* status);
+int hb_plan_phase_bits_host(const int64_t* inverse_original, const int64_t* physical_original_blocks,
+                            const int64_t* original_to_physical, int32_t grid_size,
+                            int32_t tile_count, int32_t text_tokens, int32_t block_size,
+                            int32_t shared_blocks, int32_t phase, int32_t bridge_mode, int32_t k,
+                            int32_t* scores, int64_t* bridge_original_blocks, uint32_t* bits);
+int hb_table_bits_host(const int32_t* kv_indices, const int32_t* kv_counts, int32_t rows,
+                       int32_t width, int32_t total_blocks, uint32_t* bits);
+int hb_bits_counts_host(const uint32_t* bits, int32_t rows, int32_t total_blocks,
+                        int32_t key_block_size, int32_t* counts, int32_t* paired_counts,
+                        int32_t* max_counts);
+int hb_bits_emit_host(const uint32_t* bits, int32_t rows, int32_t total_blocks,
+                      int32_t key_block_size, int32_t* ids, int32_t width, int32_t* paired_ids,
+                      int32_t* paired_flags, int32_t paired_width);
+int hb_pair_rows_host(const int32_t* kv_indices, const int32_t* kv_counts, int32_t rows,
+                      int32_t width, int32_t total_blocks, int32_t key_block_size,
+                      int32_t* paired_ids, int32_t* paired_flags, int32_t* paired_counts,
+                      int32_t paired_width, int32_t* overflow);
 
 /* ---------------------------------------------------------------- measurement
  * Dense bf16 MFMA peak probe: `groups` workgroups (0 = two per compute unit) of four waves, each

@@ -84,3 +84,27 @@ def reference(q, k, v, plan, phase, heads=None, device="cpu"):
     p = plan["phases"][phase]
     return A.block_sparse_attention(q.to(device), k.to(device), v.to(device), p["kv_indices"],
                                     p["kv_counts"], global_tokens=plan["global_tokens"], heads=heads)
+
+
+def eq_exact(a, b, what):
+    """Bit-exact comparison of a table (tensor on any device, or array) with an oracle array."""
+    a = a.cpu().numpy() if isinstance(a, torch.Tensor) else np.asarray(a)
+    b = np.asarray(b)
+    assert a.shape == b.shape, f"{what}: shape {a.shape} != {b.shape}"
+    assert a.dtype == b.dtype or (a.dtype.kind == b.dtype.kind == "i"), f"{what}: dtype {a.dtype} {b.dtype}"
+    assert np.array_equal(a, b), f"{what}: values differ at {np.argwhere(a != b)[:5].tolist()}"
+
+
+def plan_eq(dev, ref, what, directed):
+    """An AttentionPlan against the oracle's plan dict: geometry, orders, every phase's tables."""
+    assert dev.grid_size == ref["grid_size"] and dev.tile_count == ref["tile_count"]
+    assert dev.shared_tokens == ref["shared_tokens"] and dev.global_tokens == ref["global_tokens"]
+    for f in ("image_order", "inverse_image_order", "original_order", "physical_original_blocks"):
+        eq_exact(getattr(dev, f), ref[f], f"{what} {f}")
+        assert getattr(dev, f).dtype == torch.int64
+    for i, (p, r) in enumerate(zip(dev.phases, ref["phases"])):
+        assert p.offset == r["offset"]
+        assert p.kv_indices.dtype == torch.int32 and p.kv_counts.dtype == torch.int32
+        eq_exact(p.kv_indices, r["kv_indices"], f"{what} phase {i} kv_indices")
+        eq_exact(p.kv_counts, r["kv_counts"], f"{what} phase {i} kv_counts")
+        eq_exact(p.bridge_original_blocks, r["bridge_original_blocks"], f"{what} phase {i} bridges")

@@ -16,7 +16,7 @@ def test_library_exports_every_declared_symbol():
     missing = [name for name in declared if not hasattr(lib, name)]
     assert not missing, missing
     assert set(declared) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
-    assert lib.hb_version() == _lib.header_abi_version() == 3
+    assert lib.hb_version() == _lib.header_abi_version() == 4
 
 
 def test_workspace_size_and_rejections():

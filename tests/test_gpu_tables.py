@@ -5,31 +5,9 @@ import pytest
 import torch
 
 from oracle import topology as T
-from tests.helpers import oracle_paired, oracle_plan, say
+from tests.helpers import eq_exact as _eq, oracle_paired, oracle_plan, plan_eq as _plan_eq, say
 
 pytestmark = pytest.mark.gpu
-
-
-def _eq(a, b, what):
-    a = a.cpu().numpy() if isinstance(a, torch.Tensor) else np.asarray(a)
-    b = np.asarray(b)
-    assert a.shape == b.shape, f"{what}: shape {a.shape} != {b.shape}"
-    assert a.dtype == b.dtype or (a.dtype.kind == b.dtype.kind == "i"), f"{what}: dtype {a.dtype} {b.dtype}"
-    assert np.array_equal(a, b), f"{what}: values differ at {np.argwhere(a != b)[:5].tolist()}"
-
-
-def _plan_eq(dev, ref, what, directed):
-    assert dev.grid_size == ref["grid_size"] and dev.tile_count == ref["tile_count"]
-    assert dev.shared_tokens == ref["shared_tokens"] and dev.global_tokens == ref["global_tokens"]
-    for f in ("image_order", "inverse_image_order", "original_order", "physical_original_blocks"):
-        _eq(getattr(dev, f), ref[f], f"{what} {f}")
-        assert getattr(dev, f).dtype == torch.int64
-    for i, (p, r) in enumerate(zip(dev.phases, ref["phases"])):
-        assert p.offset == r["offset"]
-        assert p.kv_indices.dtype == torch.int32 and p.kv_counts.dtype == torch.int32
-        _eq(p.kv_indices, r["kv_indices"], f"{what} phase {i} kv_indices")
-        _eq(p.kv_counts, r["kv_counts"], f"{what} phase {i} kv_counts")
-        _eq(p.bridge_original_blocks, r["bridge_original_blocks"], f"{what} phase {i} bridges")
 
 
 @pytest.mark.parametrize("grid", [2, 4, 8, 64, 128, 256])
@@ -348,3 +326,53 @@ def test_pair_rows_beyond_2048_key_blocks(hip_device):
     assert np.array_equal(pct, ref["kv_counts"])
     assert np.array_equal(pid[:, :rw], ref["kv_indices"]) and np.array_equal(pfl[:, :rw], ref["kv_flags"])
     assert not pid[:, rw:].any() and not pfl[:, rw:].any()
+
+
+@pytest.mark.parametrize("grid,tiles,k,shared,key_block", [
+    (128, 16, 3, True, 128), (256, 16, 4, True, 64), (512, 16, 3, False, 64)])
+def test_host_and_device_builders_agree(hip_device, grid, tiles, k, shared, key_block):
+    """The host builder (device="cpu") and the fused device plan write the same layout and paired
+    tables bit for bit, up to 8192 px (4096 image blocks), beyond the oracle-checked sizes; and
+    the same unpaired tables through build_plan / bridge_k_plan."""
+    from hilberta_amd.bridge_k import bridge_k_plan, paired_plan_device
+
+    say(f"case host==device grid={grid} tiles={tiles} K={k} shared={shared} KB{key_block}")
+    dev = paired_plan_device(tiles, k, shared, grid_size=grid, key_block_size=key_block,
+                             device=hip_device)
+    host = paired_plan_device(tiles, k, shared, grid_size=grid, key_block_size=key_block,
+                              device="cpu")
+    for f in ("original_order", "inverse_original", "image_order", "inverse_image_order",
+              "physical_original_blocks", "original_to_physical"):
+        _eq(getattr(dev.layout, f), getattr(host.layout, f).numpy(), f)
+    for phase, (d, h) in enumerate(zip(dev.phases, host.phases)):
+        for f in ("kv_indices", "kv_flags", "kv_counts"):
+            _eq(getattr(d, f), getattr(h, f).numpy(), f"phase {phase} {f}")
+    if grid <= 256:
+        d = bridge_k_plan(tiles, k, shared, grid_size=grid, device=hip_device)
+        h = bridge_k_plan(tiles, k, shared, grid_size=grid, device="cpu")
+        for pd, ph in zip(d.phases, h.phases):
+            _eq(pd.kv_indices, ph.kv_indices.numpy(), "bridge_k kv_indices")
+            _eq(pd.bridge_original_blocks, ph.bridge_original_blocks.numpy(), "bridges")
+
+
+@pytest.mark.parametrize("rows,kb", [(4001, 64), (4000, 128)])
+def test_host_and_device_pair_rows_agree(hip_device, rows, kb):
+    """hb_pair_rows and hb_pair_rows_host on random ragged tables over ~4000 key blocks (odd and
+    even row counts), garbage past each count included: identical ids, flags, counts and overflow."""
+    from hilberta_amd._tables import pair_rows_device
+
+    rng = np.random.default_rng(rows + kb)
+    T_ = rows + 8
+    width = 24
+    ids = rng.integers(-3, T_ + 3, size=(rows, width), dtype=np.int32)
+    counts = rng.integers(0, width + 3, size=rows, dtype=np.int32)
+    say(f"case pair_rows host==device rows={rows} KB{kb}")
+    for pwidth in (2 * width, 9):
+        outs = []
+        for device in (hip_device, torch.device("cpu")):
+            flag = torch.zeros((), dtype=torch.int32, device=device)
+            got = pair_rows_device(torch.from_numpy(ids).to(device), torch.from_numpy(counts).to(device),
+                                   T_, key_block_size=kb, paired_width=pwidth, overflow=flag)
+            outs.append([x.cpu().numpy() for x in got] + [int(flag)])
+        for a, b, what in zip(outs[0], outs[1], ("ids", "flags", "counts", "overflow")):
+            assert np.array_equal(a, b), f"{what} differ at width {pwidth}"
