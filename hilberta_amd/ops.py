@@ -3,7 +3,8 @@
 The reference launches its kernels as framework-visible Triton launches (paired_kernel.py:181-204,
 sparse_kernel.py:315-339) and gathers with ``index_select`` (flux_adapter.py:209-212, :243).
 Here each HIP entry point of include/hilberta_hip.h is a registered operator with a schema, a
-fake (shape-only) implementation for tracing, and a real implementation for HIP devices only:
+fake (shape-only) implementation for tracing, and a real implementation for HIP devices (and,
+for pair_rows alone, for the CPU):
 
   hilberta_hip::paired_fwd(q, k, v, out!, lse!?, kv_indices, kv_flags, kv_counts, global_tokens,
                            key_block_size, scale_log2, all_queries, num_groups) -> ()
@@ -16,7 +17,9 @@ fake (shape-only) implementation for tracing, and a real implementation for HIP 
 The attention ops write into caller-provided outputs (declared mutated), as the reference's
 launches write into ``out``.  Argument checks with the reference's messages stay in the Python
 entry points (paired_attention, sparse_attention) and run before the op; the library repeats the
-cheap ones and reports them as ValueError.  There is no CPU kernel: on CPU tensors the ops raise.
+cheap ones and reports them as ValueError.  The attention and gather ops have no CPU kernel: on
+CPU tensors they raise.  pair_rows is plan setup and also runs on CPU tensors, through the
+library's host table builder (hb_pair_rows_host, bit-identical to the device kernel).
 """
 
 import ctypes
@@ -116,12 +119,13 @@ def _(q, k, v, out, lse, kv_indices, kv_counts, global_tokens, scale_log2, all_q
     return None
 
 
-@torch.library.custom_op(f"{_NS}::pair_rows", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(f"{_NS}::pair_rows", mutates_args=(), device_types=("cuda", "cpu"))
 def pair_rows(kv_indices: Tensor, kv_counts: Tensor, total_blocks: int, key_block_size: int,
               paired_width: int) -> tuple[Tensor, Tensor, Tensor]:
     """hb_pair_rows: rows 2r and 2r + 1 of an unpaired table become paired row r (ids, flags with
     bit half + 2*key_half, counts), ascending and zero-padded (paired_metadata.py:26-51); an odd
-    row count is paired from the end, paired row 0 holding an empty half 0."""
+    row count is paired from the end, paired row 0 holding an empty half 0.  CPU tensors are
+    paired by hb_pair_rows_host."""
     from ._tables import pair_rows_device
 
     return pair_rows_device(kv_indices, kv_counts, total_blocks, key_block_size=key_block_size,

@@ -1,6 +1,6 @@
 """The torch custom ops (hilberta_amd/ops.py) on the CPU: schemas, fake implementations under
-FakeTensorMode (shapes only, no kernel), no CPU kernel, and the entry points' routing through
-the ops.  Real launches and torch.library.opcheck run in tests/test_gpu_ops.py."""
+FakeTensorMode (shapes only, no kernel), no CPU kernel for the attention and gather ops (pair_rows,
+plan setup, has one), and the entry points' routing through the ops.  Real launches and torch.library.opcheck run in tests/test_gpu_ops.py."""
 
 from unittest.mock import patch
 
@@ -44,6 +44,28 @@ def test_no_cpu_kernel():
     x = torch.zeros(4, 3)
     with pytest.raises(NotImplementedError):
         OPS.gather_rows(x, 0, torch.arange(4))
+
+
+def test_pair_rows_op_on_cpu_tensors():
+    """pair_rows is plan setup: on CPU tensors it runs the host builder and equals the oracle's
+    pair_metadata (reference paired_metadata.py:26-51)."""
+    from oracle import topology as T
+
+    plan = T.bridge_k_plan(16, 3, False, grid_size=64)
+    p = plan["phases"][1]
+    ref = T.pair_metadata(p["kv_indices"], p["kv_counts"], tokens=plan["total_tokens"],
+                          global_tokens=plan["global_tokens"], key_block_size=128)
+    width = ref["kv_indices"].shape[1]
+    ids, flags, counts = OPS.pair_rows(torch.from_numpy(p["kv_indices"]),
+                                       torch.from_numpy(p["kv_counts"]),
+                                       plan["total_tokens"] // 64, 128, width)
+    assert ids.device.type == "cpu"
+    assert ids.numpy().tolist() == ref["kv_indices"].tolist()
+    assert flags.numpy().tolist() == ref["kv_flags"].tolist()
+    assert counts.numpy().tolist() == ref["kv_counts"].tolist()
+    torch.library.opcheck(OPS.pair_rows.default, (torch.from_numpy(p["kv_indices"]),
+                                                  torch.from_numpy(p["kv_counts"]),
+                                                  plan["total_tokens"] // 64, 128, width))
 
 
 def test_entry_points_call_the_ops():
