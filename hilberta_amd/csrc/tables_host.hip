@@ -11,6 +11,8 @@
 // distinct keys.
 #include <string.h>
 
+#include <algorithm>
+#include <new>
 #include <vector>
 
 #include "common.h"
@@ -22,6 +24,17 @@ namespace {
 
 // key blocks per row the device pairing kernel covers; the host accepts the same tables
 constexpr int PAIR_MAX_BLOCKS = 16384;
+
+// Runs f, turning a failed host allocation into an error code: nothing throws across the C ABI.
+template <class F>
+int guarded(F&& f) {
+  try {
+    return f();
+  } catch (const std::bad_alloc&) {
+    set_error("host allocation failed");
+    return HB_EINVAL;
+  }
+}
 
 void composite_order(int g, int64_t* original, int64_t* inverse) {
   const int64_t n = (int64_t)g * g, half = n / 2;
@@ -101,46 +114,48 @@ extern "C" int hb_plan_layout_host(int32_t grid_size, int32_t block_size, int32_
                  physical_original_blocks && original_to_physical && status,
              "null output");
   const int g = grid_size, bs = block_size, nb = (int)(n / bs), text_blocks = text_tokens / bs;
-  composite_order(g, original_order, inverse_original);
-  // shared blocks: every token inside the centre square [3g/8, 5g/8)^2 (plan.py:138-150)
-  const int start = 3 * g / 8, end = 5 * g / 8;
-  std::vector<char> is_shared(nb, 0);
-  int n_shared = 0, partial = 0;
-  for (int b = 0; b < nb; ++b) {
-    int cnt = 0;
-    if (shared) {
-      for (int j = 0; j < bs; ++j) {
-        const int64_t tok = original_order[(int64_t)b * bs + j];
-        const int y = (int)(tok / g), x = (int)(tok % g);
-        cnt += (y >= start && y < end && x >= start && x < end);
+  return guarded([&] {
+    composite_order(g, original_order, inverse_original);
+    // shared blocks: every token inside the centre square [3g/8, 5g/8)^2 (plan.py:138-150)
+    const int start = 3 * g / 8, end = 5 * g / 8;
+    std::vector<char> is_shared(nb, 0);
+    int n_shared = 0, partial = 0;
+    for (int b = 0; b < nb; ++b) {
+      int cnt = 0;
+      if (shared) {
+        for (int j = 0; j < bs; ++j) {
+          const int64_t tok = original_order[(int64_t)b * bs + j];
+          const int y = (int)(tok / g), x = (int)(tok % g);
+          cnt += (y >= start && y < end && x >= start && x < end);
+        }
       }
+      if (cnt != 0 && cnt != bs) partial = 1;
+      is_shared[b] = cnt == bs;
+      n_shared += cnt == bs;
     }
-    if (cnt != 0 && cnt != bs) partial = 1;
-    is_shared[b] = cnt == bs;
-    n_shared += cnt == bs;
-  }
-  // stable partition, shared blocks first
-  int sh = 0, ord = n_shared;
-  for (int b = 0; b < nb; ++b) {
-    const int slot = is_shared[b] ? sh++ : ord++;
-    physical_original_blocks[slot] = b;
-    original_to_physical[b] = slot + text_blocks;
-  }
-  for (int64_t i = 0; i < n; ++i) inverse_image_order[i] = -1;
-  for (int64_t i = 0; i < n; ++i) {
-    const int64_t tok = original_order[physical_original_blocks[i / bs] * bs + i % bs];
-    image_order[i] = tok;
-    if (tok >= 0 && tok < n) inverse_image_order[tok] = i;
-  }
-  int bad = 0;
-  for (int64_t i = 0; i < n; ++i) {
-    const int64_t tok = image_order[i];
-    bad |= tok < 0 || tok >= n || inverse_image_order[tok] != i;
-  }
-  status[0] = n_shared;
-  status[1] = partial;
-  status[2] = bad;
-  return HB_OK;
+    // stable partition, shared blocks first
+    int sh = 0, ord = n_shared;
+    for (int b = 0; b < nb; ++b) {
+      const int slot = is_shared[b] ? sh++ : ord++;
+      physical_original_blocks[slot] = b;
+      original_to_physical[b] = slot + text_blocks;
+    }
+    for (int64_t i = 0; i < n; ++i) inverse_image_order[i] = -1;
+    for (int64_t i = 0; i < n; ++i) {
+      const int64_t tok = original_order[physical_original_blocks[i / bs] * bs + i % bs];
+      image_order[i] = tok;
+      if (tok >= 0 && tok < n) inverse_image_order[tok] = i;
+    }
+    int bad = 0;
+    for (int64_t i = 0; i < n; ++i) {
+      const int64_t tok = image_order[i];
+      bad |= tok < 0 || tok >= n || inverse_image_order[tok] != i;
+    }
+    status[0] = n_shared;
+    status[1] = partial;
+    status[2] = bad;
+    return HB_OK;
+  });
 }
 
 extern "C" int hb_plan_phase_bits_host(const int64_t* inverse_original,
@@ -173,69 +188,71 @@ extern "C" int hb_plan_phase_bits_host(const int64_t* inverse_original,
   // base rows (plan.py:173-183): the global prefix, then every ordinary block with the row's tile
   // label; the rows of one label are equal, so each label's row is built once and copied
   const int labels = tile_count;
-  std::vector<uint32_t> label_rows((size_t)labels * words, 0u);
-  for (int p = 0; p < gb; ++p)
-    for (int l = 0; l < labels; ++l) label_rows[(size_t)l * words + p / 32] |= 1u << (p % 32);
-  std::vector<int> block_label(T, -1);
-  for (int p = gb; p < T; ++p) {
-    const int l = tile_label(physical_original_blocks[p - text_blocks] * bs, off, n, width);
-    block_label[p] = l;
-    label_rows[(size_t)l * words + p / 32] |= 1u << (p % 32);
-  }
-  for (int r = 0; r < nq; ++r)
-    memcpy(bits + (int64_t)r * words, &label_rows[(size_t)block_label[gb + r] * words],
-           sizeof(uint32_t) * words);
-  if (!bridge_mode) return HB_OK;
-  // bridge scores: cross-tile 4-neighbour token pairs between two original blocks, counted in
-  // both directions (bridge_k.py:22-28)
-  memset(scores, 0, sizeof(int32_t) * (size_t)nb * nb);
-  for (int64_t y = 0; y < g; ++y)
-    for (int64_t x = 0; x < g; ++x) {
-      const int64_t a = y * g + x;
-      for (int dir = 0; dir < 2; ++dir) {
-        if (dir == 0 ? x + 1 >= g : y + 1 >= g) continue;
-        const int64_t c = dir == 0 ? a + 1 : a + g;
-        const int64_t pa = inverse_original[a], pc = inverse_original[c];
-        if (tile_label(pa, off, n, width) == tile_label(pc, off, n, width)) continue;
-        const int ba = (int)(pa / bs), bc = (int)(pc / bs);
-        ++scores[(int64_t)ba * nb + bc];
-        ++scores[(int64_t)bc * nb + ba];
+  return guarded([&] {
+    std::vector<uint32_t> label_rows((size_t)labels * words, 0u);
+    for (int p = 0; p < gb; ++p)
+      for (int l = 0; l < labels; ++l) label_rows[(size_t)l * words + p / 32] |= 1u << (p % 32);
+    std::vector<int> block_label(T, -1);
+    for (int p = gb; p < T; ++p) {
+      const int l = tile_label(physical_original_blocks[p - text_blocks] * bs, off, n, width);
+      block_label[p] = l;
+      label_rows[(size_t)l * words + p / 32] |= 1u << (p % 32);
+    }
+    for (int r = 0; r < nq; ++r)
+      memcpy(bits + (int64_t)r * words, &label_rows[(size_t)block_label[gb + r] * words],
+             sizeof(uint32_t) * words);
+    if (!bridge_mode) return HB_OK;
+    // bridge scores: cross-tile 4-neighbour token pairs between two original blocks, counted in
+    // both directions (bridge_k.py:22-28)
+    memset(scores, 0, sizeof(int32_t) * (size_t)nb * nb);
+    for (int64_t y = 0; y < g; ++y)
+      for (int64_t x = 0; x < g; ++x) {
+        const int64_t a = y * g + x;
+        for (int dir = 0; dir < 2; ++dir) {
+          if (dir == 0 ? x + 1 >= g : y + 1 >= g) continue;
+          const int64_t c = dir == 0 ? a + 1 : a + g;
+          const int64_t pa = inverse_original[a], pc = inverse_original[c];
+          if (tile_label(pa, off, n, width) == tile_label(pc, off, n, width)) continue;
+          const int ba = (int)(pa / bs), bc = (int)(pc / bs);
+          ++scores[(int64_t)ba * nb + bc];
+          ++scores[(int64_t)bc * nb + ba];
+        }
+      }
+    // top-K key blocks of each query block by (-score, (key - offset/bs) mod nb) (bridge_k.py:36-40):
+    // code (score << 32 | nb-1-rolled) is distinct per key, so the K largest codes are the picks
+    const int offset_blocks = (int)(off / bs);
+    for (int q = 0; q < nb; ++q) {
+      uint64_t top[4] = {0, 0, 0, 0};  // descending
+      const int32_t* row = scores + (int64_t)q * nb;
+      for (int key = 0; key < nb; ++key) {
+        const int s = row[key];
+        if (s <= 0) continue;
+        const int rolled = ((key - offset_blocks) % nb + nb) % nb;
+        uint64_t code = ((uint64_t)(uint32_t)s << 32) | (uint32_t)(nb - 1 - rolled);
+        for (int j = 0; j < k; ++j)
+          if (code > top[j]) {
+            const uint64_t t = top[j];
+            top[j] = code;
+            code = t;
+          }
+      }
+      for (int j = 0; j < k; ++j) {
+        int64_t chosen = -1;
+        if (top[j]) chosen = ((nb - 1 - (int)(top[j] & 0xffffffffu)) + offset_blocks) % nb;
+        bridge_original_blocks[(int64_t)q * k + j] = chosen;
       }
     }
-  // top-K key blocks of each query block by (-score, (key - offset/bs) mod nb) (bridge_k.py:36-40):
-  // code (score << 32 | nb-1-rolled) is distinct per key, so the K largest codes are the picks
-  const int offset_blocks = (int)(off / bs);
-  for (int q = 0; q < nb; ++q) {
-    uint64_t top[4] = {0, 0, 0, 0};  // descending
-    const int32_t* row = scores + (int64_t)q * nb;
-    for (int key = 0; key < nb; ++key) {
-      const int s = row[key];
-      if (s <= 0) continue;
-      const int rolled = ((key - offset_blocks) % nb + nb) % nb;
-      uint64_t code = ((uint64_t)(uint32_t)s << 32) | (uint32_t)(nb - 1 - rolled);
-      for (int j = 0; j < k; ++j)
-        if (code > top[j]) {
-          const uint64_t t = top[j];
-          top[j] = code;
-          code = t;
-        }
+    // bridge bits: directed (query -> key) or reciprocal (both directions, bridge_k.py:44)
+    for (int64_t idx = 0; idx < (int64_t)nb * k; ++idx) {
+      const int64_t key = bridge_original_blocks[idx];
+      if (key < 0) continue;
+      const int pq = (int)original_to_physical[idx / k];
+      const int pk = (int)original_to_physical[key];
+      if (pq >= gb) bits[(int64_t)(pq - gb) * words + pk / 32] |= 1u << (pk % 32);
+      if (bridge_mode == 2 && pk >= gb) bits[(int64_t)(pk - gb) * words + pq / 32] |= 1u << (pq % 32);
     }
-    for (int j = 0; j < k; ++j) {
-      int64_t chosen = -1;
-      if (top[j]) chosen = ((nb - 1 - (int)(top[j] & 0xffffffffu)) + offset_blocks) % nb;
-      bridge_original_blocks[(int64_t)q * k + j] = chosen;
-    }
-  }
-  // bridge bits: directed (query -> key) or reciprocal (both directions, bridge_k.py:44)
-  for (int64_t idx = 0; idx < (int64_t)nb * k; ++idx) {
-    const int64_t key = bridge_original_blocks[idx];
-    if (key < 0) continue;
-    const int pq = (int)original_to_physical[idx / k];
-    const int pk = (int)original_to_physical[key];
-    if (pq >= gb) bits[(int64_t)(pq - gb) * words + pk / 32] |= 1u << (pk % 32);
-    if (bridge_mode == 2 && pk >= gb) bits[(int64_t)(pk - gb) * words + pq / 32] |= 1u << (pq % 32);
-  }
-  return HB_OK;
+    return HB_OK;
+  });
 }
 
 extern "C" int hb_table_bits_host(const int32_t* kv_indices, const int32_t* kv_counts, int32_t rows,
@@ -312,24 +329,26 @@ extern "C" int hb_pair_rows_host(const int32_t* kv_indices, const int32_t* kv_co
   const int lead = rows & 1, prows = (rows + 1) / 2, ratio = key_block_size / 64;
   // two bitmap rows, one word beyond the last key block (pair_flag reads up to bit T)
   const int words = total_blocks / 32 + 2;
-  std::vector<uint32_t> bm(2 * (size_t)words);
-  for (int pr = 0; pr < prows; ++pr) {
-    std::fill(bm.begin(), bm.end(), 0u);
-    for (int h = 0; h < 2; ++h) {
-      const int row = 2 * pr + h - lead;
-      if (row < 0) continue;
-      int c = kv_counts[row] < width ? kv_counts[row] : width;
-      if (c < 0) c = 0;
-      for (int e = 0; e < c; ++e) {
-        const int p = kv_indices[(int64_t)row * width + e];
-        if (p >= 0 && p < total_blocks) bm[(size_t)h * words + p / 32] |= 1u << (p % 32);
+  return guarded([&] {
+    std::vector<uint32_t> bm(2 * (size_t)words);
+    for (int pr = 0; pr < prows; ++pr) {
+      std::fill(bm.begin(), bm.end(), 0u);
+      for (int h = 0; h < 2; ++h) {
+        const int row = 2 * pr + h - lead;
+        if (row < 0) continue;
+        int c = kv_counts[row] < width ? kv_counts[row] : width;
+        if (c < 0) c = 0;
+        for (int e = 0; e < c; ++e) {
+          const int p = kv_indices[(int64_t)row * width + e];
+          if (p >= 0 && p < total_blocks) bm[(size_t)h * words + p / 32] |= 1u << (p % 32);
+        }
       }
+      const int n = emit_row(bm.data(), words, total_blocks, 1, ratio, 0,
+                             paired_ids + (int64_t)pr * paired_width,
+                             paired_flags + (int64_t)pr * paired_width, paired_width);
+      paired_counts[pr] = n < paired_width ? n : paired_width;
+      if (n > paired_width && overflow) *overflow |= 1;
     }
-    const int n = emit_row(bm.data(), words, total_blocks, 1, ratio, 0,
-                           paired_ids + (int64_t)pr * paired_width,
-                           paired_flags + (int64_t)pr * paired_width, paired_width);
-    paired_counts[pr] = n < paired_width ? n : paired_width;
-    if (n > paired_width && overflow) *overflow |= 1;
-  }
-  return HB_OK;
+    return HB_OK;
+  });
 }
