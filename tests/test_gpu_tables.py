@@ -328,26 +328,27 @@ def test_pair_rows_beyond_2048_key_blocks(hip_device):
     assert not pid[:, rw:].any() and not pfl[:, rw:].any()
 
 
-@pytest.mark.parametrize("grid,tiles,k,shared,key_block", [
-    (128, 16, 3, True, 128), (256, 16, 4, True, 64), (512, 16, 3, False, 64)])
-def test_host_and_device_builders_agree(hip_device, grid, tiles, k, shared, key_block):
+@pytest.mark.parametrize("grid,tiles,k,shared,key_block,text", [
+    (128, 16, 3, True, 128, 512), (256, 16, 4, True, 64, 512), (512, 16, 3, False, 64, 512),
+    (64, 16, 2, False, 64, 256), (128, 4, 4, True, 128, 1024), (256, 64, 1, False, 128, 128)])
+def test_host_and_device_builders_agree(hip_device, grid, tiles, k, shared, key_block, text):
     """The host builder (device="cpu") and the fused device plan write the same layout and paired
     tables bit for bit, up to 8192 px (4096 image blocks), beyond the oracle-checked sizes; and
     the same unpaired tables through build_plan / bridge_k_plan."""
     from hilberta_amd.bridge_k import bridge_k_plan, paired_plan_device
 
-    say(f"case host==device grid={grid} tiles={tiles} K={k} shared={shared} KB{key_block}")
-    dev = paired_plan_device(tiles, k, shared, grid_size=grid, key_block_size=key_block,
-                             device=hip_device)
-    host = paired_plan_device(tiles, k, shared, grid_size=grid, key_block_size=key_block,
-                              device="cpu")
+    say(f"case host==device grid={grid} tiles={tiles} K={k} shared={shared} KB{key_block} text={text}")
+    dev = paired_plan_device(tiles, k, shared, grid_size=grid, text_tokens=text,
+                             key_block_size=key_block, device=hip_device)
+    host = paired_plan_device(tiles, k, shared, grid_size=grid, text_tokens=text,
+                              key_block_size=key_block, device="cpu")
     for f in ("original_order", "inverse_original", "image_order", "inverse_image_order",
               "physical_original_blocks", "original_to_physical"):
         _eq(getattr(dev.layout, f), getattr(host.layout, f).numpy(), f)
     for phase, (d, h) in enumerate(zip(dev.phases, host.phases)):
         for f in ("kv_indices", "kv_flags", "kv_counts"):
             _eq(getattr(d, f), getattr(h, f).numpy(), f"phase {phase} {f}")
-    if grid <= 256:
+    if grid <= 256 and text == 512:  # bridge_k_plan has the reference's fixed 512-token prefix
         d = bridge_k_plan(tiles, k, shared, grid_size=grid, device=hip_device)
         h = bridge_k_plan(tiles, k, shared, grid_size=grid, device="cpu")
         for pd, ph in zip(d.phases, h.phases):

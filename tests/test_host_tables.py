@@ -213,3 +213,41 @@ def test_default_device_without_gpu_names_the_host_builder():
 
     with pytest.raises(RuntimeError, match="device='cpu'"):
         hilbert_order(8)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_pair_metadata_host_random_tables(seed):
+    """Random valid tables (global prefix, unique ids in any order, ragged counts, garbage past
+    each count) on random geometries: pair_metadata(device="cpu") and hb_pair_rows_host both
+    equal the oracle's pair_metadata, at 64- and 128-token key blocks."""
+    from hilberta_amd._tables import pair_rows_device
+    from hilberta_amd.paired_metadata import pair_metadata
+
+    rng = np.random.default_rng(seed)
+    G = 128 * int(rng.integers(0, 5))
+    rows = 2 * int(rng.integers(1, 40))
+    N = G + 64 * rows
+    T_ = N // 64
+    width = G // 64 + int(rng.integers(1, 24))
+    ids = np.full((rows, width), -1, np.int32)
+    counts = np.zeros(rows, np.int32)
+    for r in range(rows):
+        extra = rng.choice(np.arange(G // 64, T_), size=int(rng.integers(1, min(width - G // 64, T_ - G // 64) + 1)),
+                           replace=False)
+        row = np.concatenate([np.arange(G // 64), extra]).astype(np.int32)
+        rng.shuffle(row)
+        ids[r, :len(row)] = row
+        ids[r, len(row):] = rng.integers(0, T_, size=width - len(row))
+        counts[r] = len(row)
+    for kb in (64, 128):
+        ref = T.pair_metadata(ids, counts, tokens=N, global_tokens=G, key_block_size=kb)
+        meta = pair_metadata(torch.from_numpy(ids), torch.from_numpy(counts), tokens=N,
+                             global_tokens=G, key_block_size=kb, device=CPU)
+        for f in ("kv_indices", "kv_flags", "kv_counts"):
+            eq_exact(getattr(meta, f), ref[f], f"seed {seed} KB{kb} {f}")
+        w = ref["kv_indices"].shape[1]
+        pid, pfl, pct = pair_rows_device(torch.from_numpy(ids), torch.from_numpy(counts), T_,
+                                         key_block_size=kb, paired_width=w)
+        eq_exact(pid, ref["kv_indices"], "pair_rows ids")
+        eq_exact(pfl, ref["kv_flags"], "pair_rows flags")
+        eq_exact(pct, ref["kv_counts"], "pair_rows counts")
