@@ -155,3 +155,42 @@ def test_paired_ragged_shapes():
     buf = ctypes.c_void_p(16)
     rc = lib.hb_pair_rows(buf, buf, -3, 4, 72, 64, buf, buf, buf, 8, None, None)
     assert rc == 1 and "rows must be positive" in _lib.last_error()
+
+
+def test_plain_c_host_builds_a_paired_phase(tmp_path):
+    """A plain C program (tests/c/host_plan.c, gcc -std=c99, the header as is) links the library,
+    builds one phase of a bridge_k plan with the host entry points and pairs it: its output equals
+    the oracle's bridge_k_plan + pair_metadata, without a GPU."""
+    import shutil
+    import subprocess
+    from pathlib import Path
+
+    import pytest
+
+    from oracle import topology as T
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc is not installed")
+    root = Path(__file__).resolve().parents[1]
+    exe = tmp_path / "host_plan"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-Werror", "-O2", f"-I{root / 'include'}",
+                    str(root / "tests" / "c" / "host_plan.c"), f"-L{root / 'hilberta_amd'}",
+                    "-lhilberta_hip", f"-Wl,-rpath,{root / 'hilberta_amd'}", "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    for grid, tiles, k, phase, kb in ((64, 16, 3, 1, 64), (128, 4, 2, 3, 128), (128, 16, 3, 2, 64)):
+        out = subprocess.run([str(exe), str(grid), str(tiles), str(k), str(phase), str(kb)],
+                             check=True, capture_output=True, text=True).stdout.splitlines()
+        plan = T.bridge_k_plan(tiles, k, False, grid_size=grid)
+        p = plan["phases"][phase]
+        ref = T.pair_metadata(p["kv_indices"], p["kv_counts"], tokens=plan["total_tokens"],
+                              global_tokens=plan["global_tokens"], key_block_size=kb)
+        assert out[0] == "shared 0"
+        rows, width = ref["kv_indices"].shape
+        assert out[1] == f"rows {rows} width {width}"
+        for r, line in enumerate(out[2:]):
+            count, _, entries = line.partition(":")
+            pairs = [tuple(map(int, e.split("/"))) for e in entries.split()]
+            assert int(count) == ref["kv_counts"][r] == len(pairs)
+            assert [b for b, _ in pairs] == ref["kv_indices"][r, :len(pairs)].tolist()
+            assert [f for _, f in pairs] == ref["kv_flags"][r, :len(pairs)].tolist()
+        assert len(out) == 2 + rows
