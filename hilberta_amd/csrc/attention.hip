@@ -33,8 +33,8 @@
 //    half the load instructions and LDS writes per MFMA of a paired item.
 //    A block that the flag test (flags >> (half + 2*key_half)) & 1 of paired_kernel.py:65,83-84
 //    hides from a wave's half is computed but masked (P = 0), which keeps one code path (a
-//    wave-uniform branch around the masked case measured slower: the compiler's schedule of the
-//    common path degrades).
+//    wave-uniform branch around the masked case measured slower, and with this compiler it
+//    spills about 280 VGPRs to scratch: the step's state stays live across both paths).
 //  * Online softmax in exp2 with fp32 state (paired_kernel.py:82-93) and a lazy rescale; P is
 //    rounded to the input type before the PV product and summed unrounded into the row
 //    normaliser, as in the reference; an optional fp32 per-row logsumexp (natural log) is written
