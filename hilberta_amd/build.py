@@ -43,9 +43,15 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP toolchain (ROCm) is required to build")
 
 
+# Per-file flags.  attention.hip: no atomic optimizer.  Its atomics are single-lane work-queue
+# claims; the optimizer turns each into a wave-aggregated atomic that reads its result back (and
+# so waits for the round trip) right after issue, where the kernel means to overlap it with a step.
+FILE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
+
+
 def _compile(src: Path) -> Path:
     obj = OUT / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
